@@ -1,0 +1,162 @@
+/*
+ * nia_attn.h - C ABI of the MI355X (gfx950) attention library for nano-inference.
+ *
+ * The library (libnia_attn.so) holds hand-written HIP kernels for the attention
+ * hot path of nano-inference and nothing else.  Every entry point:
+ *   - takes plain device pointers, sizes and element strides (no framework types);
+ *   - enqueues its kernels on the caller's HIP stream (`stream`, a hipStream_t,
+ *     NULL = the legacy default stream) and returns without synchronising;
+ *   - returns NIA_OK (0) or a nonzero status; nia_error_string() names it.
+ *     Status codes are returned for bad arguments before anything is launched,
+ *     so a caller can fail one batch without tearing the process down.
+ *   - allocates no device memory: outputs and scratch (`workspace`) belong to
+ *     the caller.
+ *
+ * Index dtypes follow the reference engine's metadata:
+ *   slot_mapping int64 with -1 padding, block tables int32 zero-padded,
+ *   context_lens int64 (src/nano_inference/engine/context_builder.py:121,154-159).
+ * KV-cache layout is one layer's slice of the allocator's pool,
+ *   [num_blocks, num_kv_heads, block_size, head_dim], contiguous
+ *   (src/nano_inference/kv_cache/allocator.py:35-39, layers/attention.py:244-245).
+ * Query head h reads KV head h / (num_heads / num_kv_heads)
+ *   (repeat_interleave at src/nano_inference/layers/attention.py:310-314).
+ *
+ * The reference engine has no native code: every function below replaces a
+ * sequence of PyTorch ops, cited per function.
+ */
+#ifndef NIA_ATTN_H
+#define NIA_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types (`dtype` arguments) */
+#define NIA_DTYPE_BF16 0
+#define NIA_DTYPE_F32 1
+
+/* causal modes (`causal` arguments of the prefill entry points) */
+#define NIA_CAUSAL_NONE 0         /* every query row sees all k_len keys            */
+#define NIA_CAUSAL_TOP_LEFT 1     /* row j sees keys [0, min(j + 1, k_len))         */
+#define NIA_CAUSAL_BOTTOM_RIGHT 2 /* row j sees keys [0, k_len - q_len + j + 1)     */
+
+/* status codes */
+#define NIA_OK 0
+#define NIA_ERR_INVALID_ARGUMENT 1 /* a null pointer, a negative size, a bad stride     */
+#define NIA_ERR_UNSUPPORTED 2      /* a shape/dtype combination with no kernel         */
+#define NIA_ERR_WORKSPACE 3        /* workspace missing or smaller than required       */
+#define NIA_ERR_LAUNCH 4           /* the HIP runtime refused the kernel launch        */
+#define NIA_ERR_MISALIGNED 5       /* a pointer or stride breaks 16-byte vector access */
+
+/* Library ABI version; bumped whenever a signature below changes. */
+int32_t nia_abi_version(void);
+
+/* Human-readable name of a status code (static storage, never NULL). */
+const char* nia_error_string(int32_t status);
+
+/*
+ * KV-cache write: scatter the step's new K/V rows into their physical slots.
+ * Replaces the per-token loop of src/nano_inference/layers/attention.py:267-278:
+ *   for each token t with slot = slot_mapping[t] >= 0:
+ *     k_cache[slot // block_size, :, slot % block_size, :] = k[t]   (same for v)
+ * The copy is bit-exact (no conversion).  Tokens with slot < 0 are skipped, as
+ * are slots >= num_blocks * block_size (the reference would raise; the Python
+ * host layer validates when asked to).
+ *   k, v          [num_tokens, num_kv_heads, head_dim] with element strides
+ *                 (k_tok_stride, k_head_stride), (v_tok_stride, v_head_stride);
+ *                 the last dimension is contiguous.
+ *   slot_mapping  [num_tokens] int64 (the reference's (B, S_step) tensor flattened).
+ */
+int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                     const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                     void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                     int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream);
+
+/*
+ * Paged decode attention: one query token per sequence against its cached keys.
+ * Replaces the decode branch of src/nano_inference/layers/attention.py:285-332
+ * (block-table gather, GQA repeat_interleave, context-length mask, and
+ * scaled_dot_product_attention at :12-50 with S_q = 1):
+ *   out[b, h] = softmax(scale * q[b, h] . K[b, :L_b]^T) V[b, :L_b]
+ * with L_b = context_lens[b] and key t of sequence b at block
+ * block_tables[b, t / block_size], offset t % block_size.
+ * Keys at t >= L_b are never read, so padded table entries (the reference reads
+ * block 0 there and masks it) cannot affect the output.  Sequences with L_b <= 0
+ * produce zeros.  Block ids outside [0, num_blocks) are skipped.
+ *   q, out       [batch, num_heads, head_dim] with element strides (batch, head).
+ *   block_tables [batch, bt_stride] int32, the first max_blocks_per_seq columns used.
+ *   workspace    >= nia_paged_decode_workspace_size(...) bytes of device memory.
+ * Supported: head_dim 128; block_size 16; num_heads / num_kv_heads in 1..8;
+ * dtype bf16 (fp32 softmax and accumulation) or f32.
+ */
+size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_heads,
+                                       int32_t max_blocks_per_seq, int32_t block_size,
+                                       int32_t head_dim);
+
+int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_stride,
+                         const void* q, int64_t q_batch_stride, int64_t q_head_stride,
+                         const void* k_cache, const void* v_cache,
+                         const int32_t* block_tables, int32_t bt_stride,
+                         int32_t max_blocks_per_seq, const int64_t* context_lens,
+                         int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                         float scale, void* workspace, size_t workspace_bytes,
+                         int32_t dtype, void* stream);
+
+/*
+ * Varlen prefill attention over contiguous K/V (causal or not).
+ * Replaces the prefill branch of src/nano_inference/layers/attention.py:281-284
+ * with scaled_dot_product_attention (:12-50, causal triu at :33-38, padding
+ * mask at :40-47), and the per-chunk loop of the vision tower
+ * (src/nano_inference/layers/vision.py:190-208, is_causal=False).
+ * Sequence s owns query rows [q_start[s], q_start[s] + q_len[s]) and key/value
+ * rows [k_start[s], k_start[s] + k_len[s]); this covers the packed cu_seqlens
+ * layout (q_start = cu[:-1]) and the reference's padded (B, S_max) layout
+ * (q_start[s] = s * S_max).  Rows are visited by token index, so q/k/v/out are
+ * [tokens, heads, head_dim] with element strides (tok, head).
+ * Query rows that see no key produce zeros.
+ *   max_q_len  upper bound of q_len[s] (sizes the grid; larger is allowed).
+ * Supported: dtype bf16; head_dim 64, 80, 96 or 128; num_heads % num_kv_heads == 0.
+ */
+int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                    const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                    const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                    const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                    const int32_t* q_start, const int32_t* q_len,
+                    const int32_t* k_start, const int32_t* k_len,
+                    int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                    int32_t num_kv_heads, int32_t head_dim, float scale, int32_t causal,
+                    int32_t dtype, void* stream);
+
+/*
+ * Chunked prefill over the paged KV cache.  Has no counterpart in the
+ * reference, whose prefill ignores the cache (src/nano_inference/layers/
+ * attention.py:281-284); it is the cache-reading generalisation of nia_prefill
+ * that chunked prefill needs.  Sequence s has q_len[s] new query rows at
+ * absolute positions context_lens[s] - q_len[s] + j (their K/V already written
+ * by nia_kv_write) and reads its keys [0, context_lens[s]) through
+ * block_tables exactly as nia_paged_decode does.  `causal` is normally
+ * NIA_CAUSAL_BOTTOM_RIGHT; NIA_CAUSAL_NONE lets every row see the whole context.
+ * Supported: dtype bf16; head_dim 64, 80, 96 or 128; block_size a power of two
+ * in 1..64.
+ */
+int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                          const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                          const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, int32_t bt_stride,
+                          int32_t max_blocks_per_seq, const int32_t* q_start,
+                          const int32_t* q_len, const int64_t* context_lens,
+                          int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int64_t num_blocks, float scale, int32_t causal, int32_t dtype,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NIA_ATTN_H */

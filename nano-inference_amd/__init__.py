@@ -1,0 +1,32 @@
+"""gfx950 (MI355X) attention path for nano-inference.
+
+Hand-written HIP kernels behind a C ABI (libnia_attn.so, include/nia_attn.h),
+with PyTorch-side layers that keep the reference engine's attention interface:
+
+* ``ops``        - tensor-level wrappers of the C ABI (kv_write, paged_decode,
+                   prefill, varlen_attention, prefill_paged);
+* ``attention``  - ``PagedCausalSelfAttention``, ``Qwen25VLDecoderAttention`` and
+                   ``scaled_dot_product_attention`` as drop-ins for
+                   src/nano_inference/layers/attention.py;
+* ``vision``     - ``VisionAttention`` (Qwen2.5-VL ViT) and its chunk producers;
+* ``context``    - ``AttentionMetadata``, field-for-field the reference's.
+"""
+from . import _lib, ops  # noqa: F401
+from .attention import (  # noqa: F401
+    PagedCausalSelfAttention,
+    Qwen25VLDecoderAttention,
+    scaled_dot_product_attention,
+)
+from .context import AttentionMetadata  # noqa: F401
+from .vision import VisionAttention, full_cu_seqlens, window_index  # noqa: F401
+
+__all__ = [
+    "ops",
+    "AttentionMetadata",
+    "PagedCausalSelfAttention",
+    "Qwen25VLDecoderAttention",
+    "scaled_dot_product_attention",
+    "VisionAttention",
+    "full_cu_seqlens",
+    "window_index",
+]

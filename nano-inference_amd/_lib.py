@@ -1,0 +1,108 @@
+"""ctypes binding of libnia_attn.so, the gfx950 attention library.
+
+The library is built in-tree (``build_lib.py``) and loaded from the package
+directory.  There is no fallback: if the library is missing, every attention
+call raises, so a GPU run can never silently take another path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+from pathlib import Path
+
+LIB_NAME = "libnia_attn.so"
+PKG_DIR = Path(os.path.realpath(__file__)).parent
+
+# Mirrors the #defines of include/nia_attn.h.
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+CAUSAL_NONE = 0
+CAUSAL_TOP_LEFT = 1
+CAUSAL_BOTTOM_RIGHT = 2
+OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_UNSUPPORTED = 2
+ERR_WORKSPACE = 3
+ERR_LAUNCH = 4
+ERR_MISALIGNED = 5
+
+_p = C.c_void_p
+_i32 = C.c_int32
+_i64 = C.c_int64
+_f32 = C.c_float
+_sz = C.c_size_t
+
+# name -> (restype, argtypes); the order of arguments is that of nia_attn.h.
+SIGNATURES = {
+    "nia_abi_version": (_i32, []),
+    "nia_error_string": (C.c_char_p, [_i32]),
+    "nia_kv_write": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i32, _p],
+    ),
+    "nia_paged_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "nia_paged_decode": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p,
+         _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _sz, _i32, _p],
+    ),
+    "nia_prefill": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64,
+         _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p],
+    ),
+    "nia_prefill_paged": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p, _p, _p,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p],
+    ),
+}
+
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib: C.CDLL | None = None
+
+
+class NiaError(RuntimeError):
+    """A nonzero status returned by the attention library."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn}: {msg} (status {status})")
+        self.status = status
+
+
+def lib_path() -> Path:
+    return PKG_DIR / LIB_NAME
+
+
+def load() -> C.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = lib_path()
+            if not path.exists():
+                raise ImportError(
+                    f"{path} is missing: build it with `python {PKG_DIR / 'build_lib.py'}` "
+                    "(or __graft_entry__.build()); there is no non-HIP attention path"
+                )
+            lib = C.CDLL(str(path))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            got = lib.nia_abi_version()
+            if got != ABI_VERSION:
+                raise ImportError(f"{path}: ABI version {got}, expected {ABI_VERSION}")
+            _lib = lib
+    return _lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != OK:
+        msg = load().nia_error_string(status).decode()
+        raise NiaError(fn, status, msg)

@@ -1,0 +1,238 @@
+"""Drop-in attention layers backed by the gfx950 kernels.
+
+Same names, constructor arguments, parameter names and forward signatures as
+the reference's src/nano_inference/layers/attention.py:
+
+* ``scaled_dot_product_attention(q, k, v, attention_mask=None, is_causal=True)``
+  (:12-50) - the free function, also used by the vision tower;
+* ``PagedCausalSelfAttention`` (:206-340) with ``.layer_idx`` and
+  ``forward(x, position_ids, attention_mask=None, metadata=None)``;
+* ``Qwen25VLDecoderAttention`` (:343-371), the mRoPE variant.
+
+Projections, QK-RMSNorm and RoPE stay PyTorch ops, as in the reference; the
+KV-cache write, the block-table gather, GQA, masking and softmax attention run
+in the HIP kernels.  Differences from the reference, all where the reference
+has no defined behaviour of its own:
+* a decode step (``is_prefill`` False) with more than one new token per
+  sequence attends with a bottom-right causal mask (chunked prefill); the
+  reference applies no causal mask when S_q != S_k
+  (src/nano_inference/layers/attention.py:33-38);
+* a padding mask must be a prefix mask (keys [0, len) visible), which is what
+  the context builder produces (src/nano_inference/engine/context_builder.py:
+  141-149); other masks raise NotImplementedError.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .context import AttentionMetadata
+from .layers import MRotaryEmbedding, RMSNorm, RotaryEmbedding
+
+
+def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int) -> torch.Tensor:
+    """Visible-key counts of a prefix mask; raises for any other mask shape.
+
+    Accepts the reference's two mask forms: 2-D bool (B, S_total) with True =
+    visible, or additive (B, 1, 1, S_total) with 0 = visible and -inf = masked.
+    """
+    if mask.dim() == 2:
+        vis = mask[:, :key_len].to(torch.bool)
+    elif mask.dim() == 4 and mask.shape[1] == 1 and mask.shape[2] == 1:
+        vis = mask[:, 0, 0, :key_len] == 0
+    else:
+        raise NotImplementedError(f"attention_mask of shape {tuple(mask.shape)}")
+    if vis.shape[0] != batch:
+        vis = vis.expand(batch, -1)
+    lens = vis.sum(dim=-1)
+    ar = torch.arange(vis.shape[-1], device=vis.device)
+    if not torch.equal(vis, ar.unsqueeze(0) < lens.unsqueeze(1)):
+        raise NotImplementedError("only prefix (right-padding) attention masks are supported")
+    return lens.to(torch.int32)
+
+
+def scaled_dot_product_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    attention_mask: Optional[torch.Tensor] = None,
+    is_causal: bool = True,
+) -> torch.Tensor:
+    """softmax(q k^T / sqrt(D) [+ causal] [+ mask]) v on the gfx950 kernel.
+
+    Shapes as in src/nano_inference/layers/attention.py:12-50: q (B, H, S_q, D),
+    k, v (B, H_kv, S_k, D) (H_kv may divide H), output (B, H, S_q, D).  As in the
+    reference the causal mask is applied only when S_q == S_k; the padding mask
+    is sliced to S_k.
+    """
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be (B, H, S, D)")
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    causal = ops.CAUSAL_TOP_LEFT if (is_causal and sq == sk) else ops.CAUSAL_NONE
+    dev = q.device
+    # (B, H, S, D) -> token-major views (B*S, H, D) when the strides allow it.
+    q3 = q.transpose(1, 2).reshape(b * sq, h, d)
+    k3 = k.transpose(1, 2).reshape(b * sk, k.shape[1], d)
+    v3 = v.transpose(1, 2).reshape(b * sk, v.shape[1], d)
+    ar = torch.arange(b, device=dev, dtype=torch.int32)
+    q_len = torch.full((b,), sq, device=dev, dtype=torch.int32)
+    if attention_mask is not None:
+        k_len = _prefix_lengths(attention_mask.to(dev), b, sk)
+    else:
+        k_len = torch.full((b,), sk, device=dev, dtype=torch.int32)
+    out = ops.prefill(q3, k3, v3, ar * sq, q_len, ar * sk, k_len, sq, causal)
+    return out.view(b, sq, h, d).transpose(1, 2)
+
+
+class CausalSelfAttentionBase(nn.Module):
+    """Marker base, as src/nano_inference/layers/attention.py:53-75."""
+
+
+class PagedCausalSelfAttention(CausalSelfAttentionBase):
+    """Paged GQA self-attention whose attention core runs on the gfx950 kernels.
+
+    Constructor and parameter names follow src/nano_inference/layers/attention.py:
+    81-140 (q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, rotary), so the
+    reference's model code and state dicts use it unchanged.
+    """
+
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        num_kv_heads: Optional[int] = None,
+        head_dim: Optional[int] = None,
+        use_qk_norm: bool = False,
+        qkv_bias: bool = False,
+        out_bias: bool = False,
+        rope_base: float = 10000.0,
+    ):
+        super().__init__()
+        if head_dim is None and hidden_size % num_heads != 0:
+            raise ValueError(
+                f"hidden_size must be divisible by num_heads, got {hidden_size=} and {num_heads=}"
+            )
+        if num_kv_heads is None:
+            num_kv_heads = num_heads
+        if num_heads % num_kv_heads != 0:
+            raise ValueError(
+                f"num_heads must be divisible by num_kv_heads, got {num_heads=} and {num_kv_heads=}"
+            )
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim if head_dim is not None else hidden_size // num_heads
+        self.use_qk_norm = use_qk_norm
+        hd = self.head_dim
+        self.q_proj = nn.Linear(hidden_size, num_heads * hd, bias=qkv_bias)
+        self.k_proj = nn.Linear(hidden_size, num_kv_heads * hd, bias=qkv_bias)
+        self.v_proj = nn.Linear(hidden_size, num_kv_heads * hd, bias=qkv_bias)
+        self.o_proj = nn.Linear(num_heads * hd, hidden_size, bias=out_bias)
+        self.q_norm = RMSNorm(hd) if use_qk_norm else None
+        self.k_norm = RMSNorm(hd) if use_qk_norm else None
+        self.rotary = RotaryEmbedding(head_dim=hd, base=rope_base)
+        self.layer_idx: Optional[int] = None
+        self._decode_ws: Optional[torch.Tensor] = None
+
+    def _apply_rotary(self, q, k, position_ids, metadata=None) -> Tuple[torch.Tensor, torch.Tensor]:
+        return self.rotary(q, k, position_ids)
+
+    def _qkv(self, x, position_ids, metadata):
+        b, s, _ = x.shape
+        q = self.q_proj(x).view(b, s, self.num_heads, self.head_dim)
+        k = self.k_proj(x).view(b, s, self.num_kv_heads, self.head_dim)
+        v = self.v_proj(x).view(b, s, self.num_kv_heads, self.head_dim)
+        if self.q_norm is not None:
+            q = self.q_norm(q)
+        if self.k_norm is not None:
+            k = self.k_norm(k)
+        q, k = self._apply_rotary(q, k, position_ids, metadata)
+        return q, k, v
+
+    def _dense_causal(self, q, k, v, attention_mask):
+        """No-cache path (metadata None): causal attention over the step's K/V."""
+        b, s = q.shape[:2]
+        dev = q.device
+        ar = torch.arange(b, device=dev, dtype=torch.int32) * s
+        lens = torch.full((b,), s, device=dev, dtype=torch.int32)
+        k_len = lens if attention_mask is None else _prefix_lengths(attention_mask.to(dev), b, s)
+        return ops.prefill(
+            q.reshape(b * s, self.num_heads, self.head_dim),
+            k.reshape(b * s, self.num_kv_heads, self.head_dim),
+            v.reshape(b * s, self.num_kv_heads, self.head_dim),
+            ar, lens, ar, k_len, s, ops.CAUSAL_TOP_LEFT,
+        )
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        position_ids: torch.Tensor,
+        attention_mask: Optional[torch.Tensor] = None,
+        metadata: Optional[AttentionMetadata] = None,
+    ) -> torch.Tensor:
+        b, s, _ = x.shape
+        q, k, v = self._qkv(x, position_ids, metadata)
+        if metadata is None:
+            attn = self._dense_causal(q, k, v, attention_mask)
+            return self.o_proj(attn.view(b, s, self.num_heads * self.head_dim))
+        assert self.layer_idx is not None, "layer_idx must be set for PagedCausalSelfAttention"
+
+        k_cache = v_cache = None
+        if metadata.k_cache is not None and metadata.v_cache is not None:
+            k_cache = metadata.k_cache[self.layer_idx]
+            v_cache = metadata.v_cache[self.layer_idx]
+
+        # 1. KV write (src/nano_inference/layers/attention.py:267-278).
+        if k_cache is not None and metadata.slot_mapping is not None:
+            ops.kv_write(k, v, k_cache, v_cache, metadata.slot_mapping)
+
+        if metadata.is_prefill:
+            # 2a. Prefill attends over the step's fresh K/V (:281-284).  Padded
+            # rows past a sequence's length see all its keys, as in the reference.
+            attn = self._dense_causal(q, k, v, attention_mask)
+        elif k_cache is not None and metadata.kv_block_tables is not None \
+                and metadata.context_lens is not None:
+            bt = metadata.kv_block_tables
+            ctx = metadata.context_lens
+            if s == 1:
+                # 2b. Decode: gather + GQA + mask + softmax in one kernel (:285-332).
+                need = ops.decode_workspace_bytes(b, self.num_heads, bt.shape[1],
+                                                  k_cache.shape[2], self.head_dim)
+                if need and (self._decode_ws is None or self._decode_ws.numel() < need
+                             or self._decode_ws.device != x.device):
+                    self._decode_ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+                attn = ops.paged_decode(q[:, 0], k_cache, v_cache, bt, ctx,
+                                        workspace=self._decode_ws)
+            else:
+                # 2c. Several new tokens on top of cached context: chunked prefill.
+                dev = x.device
+                q_len = (metadata.slot_mapping >= 0).sum(dim=1).to(torch.int32)
+                q_start = torch.arange(b, device=dev, dtype=torch.int32) * s
+                attn = torch.zeros(b * s, self.num_heads, self.head_dim, dtype=q.dtype,
+                                   device=dev)
+                ops.prefill_paged(q.reshape(b * s, self.num_heads, self.head_dim), k_cache,
+                                  v_cache, bt, q_start, q_len, ctx, s,
+                                  ops.CAUSAL_BOTTOM_RIGHT, out=attn)
+        else:
+            attn = self._dense_causal(q, k, v, attention_mask)
+        return self.o_proj(attn.reshape(b, s, self.num_heads * self.head_dim))
+
+
+class Qwen25VLDecoderAttention(PagedCausalSelfAttention):
+    """PagedCausalSelfAttention with 3-axis mRoPE (src/nano_inference/layers/attention.py:343-371)."""
+
+    def __init__(self, *args, mrope_section=(16, 24, 24), **kwargs):
+        super().__init__(*args, **kwargs)
+        self.rotary = MRotaryEmbedding(head_dim=self.head_dim, base=self.rotary.base,
+                                       mrope_section=mrope_section)
+
+    def _apply_rotary(self, q, k, position_ids, metadata=None):
+        if metadata is not None and metadata.mrope_position_ids is not None:
+            pos = metadata.mrope_position_ids
+        else:
+            pos = position_ids.unsqueeze(0).expand(3, -1, -1)
+        return self.rotary(q, k, pos)

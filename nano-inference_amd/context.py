@@ -1,0 +1,33 @@
+"""Per-step attention metadata, field-for-field the reference's contract.
+
+Mirrors ``AttentionMetadata`` of src/nano_inference/core/context.py:7-24 so that
+the reference's context builder (src/nano_inference/engine/context_builder.py:
+83-242) and inferencer (src/nano_inference/inferencer/torch_inferencer.py:
+221-222) can fill it unchanged.  The kernels read ``context_lens``,
+``kv_block_tables`` and ``slot_mapping`` directly, in the reference's dtypes.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+
+@dataclass
+class AttentionMetadata:
+    """Metadata required for paged attention (same fields as the reference)."""
+
+    context_lens: torch.Tensor  # (B,) int64 - total sequence length per request
+    kv_block_tables: torch.Tensor  # (B, max_blocks_per_seq) int32, zero-padded
+    slot_mapping: torch.Tensor  # (B, S_step) int64, -1 for padding
+
+    # Physical cache tensors [L, num_blocks, H_kv, block_size, D]
+    k_cache: Optional[torch.Tensor] = None
+    v_cache: Optional[torch.Tensor] = None
+
+    # Forward mode
+    is_prefill: bool = False
+
+    # VLM only: (3, B, S_step) mRoPE position ids; None for text-only batches.
+    mrope_position_ids: Optional[torch.Tensor] = None

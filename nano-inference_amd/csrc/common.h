@@ -1,0 +1,89 @@
+// Device helpers shared by the gfx950 attention kernels.
+//
+// Everything here targets CDNA4 (gfx950) wave64 directly: DPP row operations
+// for in-row reductions, the hardware exp2, bf16 dot2 and packed converts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nia_attn.h"
+
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+#define NIA_DEVICE __device__ __forceinline__
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- bit casts --------------------------------------------------------------
+
+NIA_DEVICE float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+NIA_DEVICE uint32_t as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+// bf16 pair packed in one dword -> two floats (exact widening).
+NIA_DEVICE float bf16_lo(uint32_t w) { return as_f32(w << 16); }
+NIA_DEVICE float bf16_hi(uint32_t w) { return as_f32(w & 0xffff0000u); }
+
+// Two floats -> bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+NIA_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = {(bf16_t)lo, (bf16_t)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// fp32 += a.lo*b.lo + a.hi*b.hi with bf16 pairs (v_dot2_f32_bf16).
+NIA_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+NIA_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- cross-lane -------------------------------------------------------------
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+NIA_DEVICE float dpp_f32(float x) {
+  return as_f32(__builtin_amdgcn_update_dpp(0, (int)as_u32(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes (N in 1,2,4,8,16,32,64); every lane of a
+// group receives the group total.  Offsets below 16 use DPP inside a row, the
+// wider ones go through the LDS crossbar (ds_bpermute).
+template <int N>
+NIA_DEVICE float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_f32<kDppQuadXor1>(x);
+  if constexpr (N >= 4) x += dpp_f32<kDppQuadXor2>(x);
+  if constexpr (N >= 8) x += dpp_f32<kDppRowHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp_f32<kDppRowMirror>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+NIA_DEVICE bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+NIA_DEVICE int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// ---- online-softmax merge -----------------------------------------------------
+
+// Merge two partial softmax states (m, l) whose values are in log2 units.
+// Returns the weights that rescale each side's accumulator.  -inf maxima
+// (no keys seen) merge to weight 0 rather than NaN.
+NIA_DEVICE void softmax_merge_weights(float m_a, float m_b, float& m, float& wa, float& wb) {
+  m = fmaxf(m_a, m_b);
+  wa = (m_a == -INFINITY) ? 0.f : fast_exp2(m_a - m);
+  wb = (m_b == -INFINITY) ? 0.f : fast_exp2(m_b - m);
+}

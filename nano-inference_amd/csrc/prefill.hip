@@ -1,0 +1,462 @@
+// Varlen prefill attention (causal / non-causal, contiguous or paged K/V) on
+// gfx950 MFMA, bf16 in, fp32 softmax and accumulation.
+//
+// Replaces, in the reference:
+//   - the prefill branch of src/nano_inference/layers/attention.py:281-284 with
+//     scaled_dot_product_attention (:12-50), which materialises (B, H, S, S)
+//     scores in bf16 and again in fp32 and applies a triu causal mask (:33-38);
+//   - the per-chunk loop of the vision tower, src/nano_inference/layers/
+//     vision.py:190-208 (non-causal, one sdpa call per image or window).
+// It also serves chunked prefill over the paged cache, which the reference
+// lacks (its prefill ignores the cache).
+//
+// Tiling (BLOCK_M = 128 query rows of one head per workgroup, 4 waves x 32 rows;
+// BLOCK_N = 64 keys per step)
+//   S^T = K Q^T with v_mfma_f32_32x32x16_bf16: A = K rows from LDS, B = Q^T held
+//   in registers for the whole kernel.  In the 32x32 accumulator layout lane l
+//   owns query column l % 32 and 16 key rows, so a query's softmax row lives in
+//   one lane pair (l, l ^ 32): row max and row sum need one cross-lane step.
+//   O^T = V^T P^T: the B operand (P^T) is the S^T accumulator converted to bf16
+//   in place, with the key order of each 16-key MFMA step permuted to match the
+//   accumulator layout; A (V^T) comes from a transposed V tile in LDS whose
+//   4-key groups are XOR-swizzled per row so that both the transposing writes
+//   and the operand reads spread over the LDS banks.  Every O^T register of a
+//   lane belongs to that lane's query, so rescaling O is lane-local.
+// Softmax: exp2 with scale * log2(e) folded into one FMA; the running max is only
+// raised when a tile's max exceeds it by more than 2^8 (lazy rescale).
+// Causal tiles above the diagonal are never visited; tiles crossing it are masked.
+// MFMA work per (query, key) pair: 4 * D flops (QK^T and PV).
+#include "common.h"
+
+namespace {
+
+constexpr int kBlockM = 128;
+constexpr int kBlockN = 64;
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillThreads = kPrefillWaves * kWave;
+constexpr float kLazyRescaleP = 8.0f;
+
+struct PrefillParams {
+  bf16_t* o;
+  int64_t o_tok, o_head;
+  const bf16_t* q;
+  int64_t q_tok, q_head;
+  const bf16_t* k;  // contiguous K/V rows, or the paged cache slice
+  int64_t k_tok, k_head;
+  const bf16_t* v;
+  int64_t v_tok, v_head;
+  const int32_t* q_start;
+  const int32_t* q_len;
+  const int32_t* k_start;  // contiguous mode
+  const int32_t* k_len;    // contiguous mode
+  const int64_t* ctx_len;  // paged mode
+  const int32_t* block_tables;
+  int32_t bt_stride;
+  int32_t max_blocks;
+  int64_t num_blocks;
+  int32_t bs_log2;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t group;
+  int32_t num_m_blocks;
+  int32_t causal;
+  float scale_log2;
+};
+
+// XOR swizzle of the 4-key groups inside a transposed-V row (row = head dim d).
+NIA_DEVICE int vt_swz(int d) { return (d ^ (d >> 3)) & 15; }
+
+template <int D, bool PAGED>
+__global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillParams p) {
+  constexpr int DK = D / 16;               // 16-wide head-dim steps of QK^T
+  constexpr int DT = (D + 31) / 32;        // 32-row head-dim tiles of O^T
+  constexpr int DP = DT * 32;              // padded head-dim rows of V^T in LDS
+  constexpr int CH = D / 8;                // 16-byte chunks per K/V row
+  constexpr int K_PITCH = 2 * D + 16;      // bytes per K row in LDS
+  constexpr int VT_PITCH = 2 * kBlockN;    // bytes per V^T row in LDS (64 keys)
+  constexpr int K_ITEMS = (kBlockN * CH + kPrefillThreads - 1) / kPrefillThreads;
+  static_assert(D % 16 == 0, "head_dim must be a multiple of 16");
+  static_assert(16 * CH <= kPrefillThreads, "V transpose: one 4-key x 8-dim item per thread");
+
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds[kBlockN * K_PITCH];
+  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[DP * VT_PITCH];
+
+  const int seq = blockIdx.z;
+  const int h = blockIdx.y;
+  const int mb = p.num_m_blocks - 1 - (int)blockIdx.x;  // long rows first
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int half = lane >> 5;
+  const int col = lane & 31;
+
+  const int qlen = p.q_len[seq];
+  const int m0 = mb * kBlockM;
+  if (m0 >= qlen) return;
+  int klen;
+  int64_t kstart = 0;
+  if constexpr (PAGED) {
+    int64_t c = p.ctx_len[seq];
+    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    klen = (int)c;
+  } else {
+    klen = p.k_len[seq];
+    kstart = p.k_start[seq];
+  }
+  const int64_t qstart = p.q_start[seq];
+  const int hk = h / p.group;
+  const bool causal = p.causal != NIA_CAUSAL_NONE;
+  const int q_pos0 = p.causal == NIA_CAUSAL_BOTTOM_RIGHT ? klen - qlen : 0;
+
+  // Keys this workgroup needs: [0, n_end).
+  int n_end = klen;
+  if (causal) n_end = min(klen, q_pos0 + min(m0 + kBlockM, qlen));
+  if (n_end < 0) n_end = 0;
+
+  // This lane's query row and key bound.
+  const int r0 = m0 + wave * 32;
+  const int qrow = r0 + col;
+  const bool row_ok = qrow < qlen;
+  const int kb = causal ? min(klen, q_pos0 + qrow + 1) : klen;
+  const int wave_kmin = causal ? min(klen, q_pos0 + r0 + 1) : klen;   // smallest bound in wave
+  const int wave_kend = r0 < qlen ? (causal ? min(klen, q_pos0 + min(r0 + 32, qlen)) : klen) : 0;
+
+  // ---- Q^T operand: DK x 8 bf16 per lane, resident for the whole kernel ----------
+  uint4 qreg[DK];
+  {
+    const bf16_t* qp = p.q + (qstart + (row_ok ? qrow : 0)) * p.q_tok + (int64_t)h * p.q_head;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      qreg[kk] = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk + 8 * half)
+                        : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  f32x16_t oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+  float m_run = -INFINITY;  // log2 units
+  float l_run = 0.f;        // partial over this lane's keys
+
+  // ---- global -> register staging of one K/V tile ------------------------------------
+  const int32_t* bt = PAGED ? p.block_tables + (int64_t)seq * p.bt_stride : nullptr;
+  auto row_ptr = [&](const bf16_t* base, int64_t tok_stride, int64_t head_stride,
+                     int n) -> const bf16_t* {
+    if constexpr (PAGED) {
+      const int blk = bt[n >> p.bs_log2];
+      if (blk < 0 || (int64_t)blk >= p.num_blocks) return nullptr;
+      const int off = n & ((1 << p.bs_log2) - 1);
+      return base + ((((int64_t)blk * p.num_kv_heads + hk) << p.bs_log2) + off) * D;
+    } else {
+      return base + (kstart + n) * tok_stride + (int64_t)hk * head_stride;
+    }
+  };
+
+  uint4 kst[K_ITEMS];
+  uint4 vst[4];
+  // V transpose item of this thread: 4 keys (4 * vkg ..) x 8 dims (8 * vdc ..)
+  const int vdc = tid % CH;
+  const int vkg = tid / CH;
+  const bool v_item = tid < 16 * CH;
+
+  auto load_tile = [&](int n0) {
+#pragma unroll
+    for (int it = 0; it < K_ITEMS; ++it) {
+      const int idx = tid + it * kPrefillThreads;
+      kst[it] = make_uint4(0, 0, 0, 0);
+      if (idx < kBlockN * CH) {
+        const int r = idx / CH;
+        const int c = idx - r * CH;
+        const int n = n0 + r;
+        if (n < klen) {
+          const bf16_t* rp = row_ptr(p.k, p.k_tok, p.k_head, n);
+          if (rp) kst[it] = *reinterpret_cast<const uint4*>(rp + 8 * c);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      vst[j] = make_uint4(0, 0, 0, 0);
+      const int n = n0 + 4 * vkg + j;
+      if (v_item && n < klen) {
+        const bf16_t* rp = row_ptr(p.v, p.v_tok, p.v_head, n);
+        if (rp) vst[j] = *reinterpret_cast<const uint4*>(rp + 8 * vdc);
+      }
+    }
+  };
+
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int it = 0; it < K_ITEMS; ++it) {
+      const int idx = tid + it * kPrefillThreads;
+      if (idx < kBlockN * CH) {
+        const int r = idx / CH;
+        const int c = idx - r * CH;
+        *reinterpret_cast<uint4*>(k_lds + r * K_PITCH + 16 * c) = kst[it];
+      }
+    }
+    if (v_item) {
+      // 4 keys x 8 dims -> for each dim, the 4 keys as one 8-byte group.
+      const uint32_t w[4][4] = {{vst[0].x, vst[0].y, vst[0].z, vst[0].w},
+                                {vst[1].x, vst[1].y, vst[1].z, vst[1].w},
+                                {vst[2].x, vst[2].y, vst[2].z, vst[2].w},
+                                {vst[3].x, vst[3].y, vst[3].z, vst[3].w}};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 8 * vdc + e;
+        const int sh = (e & 1) ? 16 : 0;
+        const uint32_t k0 = (w[0][e >> 1] >> sh) & 0xffffu;
+        const uint32_t k1 = (w[1][e >> 1] >> sh) & 0xffffu;
+        const uint32_t k2 = (w[2][e >> 1] >> sh) & 0xffffu;
+        const uint32_t k3 = (w[3][e >> 1] >> sh) & 0xffffu;
+        const uint2 val = make_uint2(k0 | (k1 << 16), k2 | (k3 << 16));
+        *reinterpret_cast<uint2*>(vt_lds + d * VT_PITCH + 8 * (vkg ^ vt_swz(d))) = val;
+      }
+    }
+  };
+
+  // Zero the padded head-dim rows of V^T once (D = 80: rows 80..95).
+  if constexpr (DP > D) {
+    for (int i = tid; i < (DP - D) * VT_PITCH / 16; i += kPrefillThreads)
+      reinterpret_cast<uint4*>(vt_lds + D * VT_PITCH)[i] = make_uint4(0, 0, 0, 0);
+  }
+
+  if (n_end > 0) load_tile(0);
+  for (int n0 = 0; n0 < n_end; n0 += kBlockN) {
+    store_tile();
+    __syncthreads();
+    if (n0 + kBlockN < n_end) load_tile(n0 + kBlockN);
+
+    if (n0 < wave_kend) {
+      // ---- S^T = K Q^T for the two 32-key halves of the tile ------------------------
+      f32x16_t sacc[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[c][r] = 0.f;
+        const uint8_t* kr = k_lds + (32 * c + col) * K_PITCH + 16 * half;
+#pragma unroll
+        for (int kk = 0; kk < DK; ++kk) {
+          const uint4 a = *reinterpret_cast<const uint4*>(kr + 32 * kk);
+          sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]),
+              sacc[c], 0, 0, 0);
+        }
+      }
+      // ---- mask, row max --------------------------------------------------------------
+      if (n0 + kBlockN > wave_kmin) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = n0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
+            if (key >= kb) sacc[c][r] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mx2 = mx * p.scale_log2;
+      if (wave_any(mx2 > m_run + kLazyRescaleP)) {
+        const float mn = fmaxf(m_run, mx2);
+        const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
+        m_run = mn;
+        l_run *= corr;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+      }
+      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+      // ---- P = exp2(S * scale - m), packed to bf16 as the B operand ------------------
+      uint4 pb[4];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p0 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub));
+            const float p1 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub));
+            l_run += p0 + p1;
+            w[j] = pack_bf16x2(p0, p1);
+          }
+          pb[2 * c + hh] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+      // ---- O^T += V^T P^T ---------------------------------------------------------------
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 32 * dt + col;
+        const uint8_t* vr = vt_lds + d * VT_PITCH;
+        const int sw = vt_swz(d);
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr + 8 * ((4 * kc + half) ^ sw));
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8 * ((4 * kc + 2 + half) ^ sw));
+          const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, pb[kc]), oacc[dt],
+              0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: normalise and store this lane's query row -----------------------------
+  if (!row_ok) return;
+  const float lt = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  bf16_t* op = p.o + (qstart + qrow) * p.o_tok + (int64_t)h * p.o_head;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * dt + 8 * g + 4 * half;
+      if (d < D) {
+        const uint2 val = make_uint2(pack_bf16x2(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv),
+                                     pack_bf16x2(oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv));
+        *reinterpret_cast<uint2*>(op + d) = val;
+      }
+    }
+  }
+}
+
+template <bool PAGED>
+int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream_t s) {
+  const dim3 grid(p.num_m_blocks, p.num_heads, num_seqs);
+  switch (head_dim) {
+    case 64:
+      hipLaunchKernelGGL((prefill_kernel<64, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
+      break;
+    case 80:
+      hipLaunchKernelGGL((prefill_kernel<80, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
+      break;
+    case 96:
+      hipLaunchKernelGGL((prefill_kernel<96, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
+      break;
+    case 128:
+      hipLaunchKernelGGL((prefill_kernel<128, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
+      break;
+    default:
+      return NIA_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+}
+
+bool supported_head_dim(int d) { return d == 64 || d == 80 || d == 96 || d == 128; }
+
+bool vec_ok(const void* ptr, int64_t a, int64_t b) {
+  return (uintptr_t)ptr % 16 == 0 && a % 8 == 0 && b % 8 == 0;
+}
+
+}  // namespace
+
+extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                               const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                               const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                               const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                               const int32_t* q_start, const int32_t* q_len,
+                               const int32_t* k_start, const int32_t* k_len, int32_t num_seqs,
+                               int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, float scale, int32_t causal, int32_t dtype,
+                               void* stream) {
+  if (num_seqs < 0 || max_q_len < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
+      num_heads % num_kv_heads != 0)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (causal < NIA_CAUSAL_NONE || causal > NIA_CAUSAL_BOTTOM_RIGHT || !(scale > 0.f) ||
+      scale == INFINITY)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (num_seqs == 0 || max_q_len == 0) return NIA_OK;
+  if (!out || !q || !k || !v || !q_start || !q_len || !k_start || !k_len)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (dtype != NIA_DTYPE_BF16 || !supported_head_dim(head_dim)) return NIA_ERR_UNSUPPORTED;
+  if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(k, k_tok_stride, k_head_stride) ||
+      !vec_ok(v, v_tok_stride, v_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride))
+    return NIA_ERR_MISALIGNED;
+  PrefillParams p{};
+  p.o = (bf16_t*)out;
+  p.o_tok = out_tok_stride;
+  p.o_head = out_head_stride;
+  p.q = (const bf16_t*)q;
+  p.q_tok = q_tok_stride;
+  p.q_head = q_head_stride;
+  p.k = (const bf16_t*)k;
+  p.k_tok = k_tok_stride;
+  p.k_head = k_head_stride;
+  p.v = (const bf16_t*)v;
+  p.v_tok = v_tok_stride;
+  p.v_head = v_head_stride;
+  p.q_start = q_start;
+  p.q_len = q_len;
+  p.k_start = k_start;
+  p.k_len = k_len;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.num_m_blocks = (max_q_len + kBlockM - 1) / kBlockM;
+  p.causal = causal;
+  p.scale_log2 = scale * kLog2e;
+  return launch_prefill<false>(p, head_dim, num_seqs, (hipStream_t)stream);
+}
+
+extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                     const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                     const void* k_cache, const void* v_cache,
+                                     const int32_t* block_tables, int32_t bt_stride,
+                                     int32_t max_blocks_per_seq, const int32_t* q_start,
+                                     const int32_t* q_len, const int64_t* context_lens,
+                                     int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int64_t num_blocks, float scale, int32_t causal,
+                                     int32_t dtype, void* stream) {
+  if (num_seqs < 0 || max_q_len < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
+      num_heads % num_kv_heads != 0 || max_blocks_per_seq < 0 ||
+      bt_stride < max_blocks_per_seq || num_blocks < 0)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (causal < NIA_CAUSAL_NONE || causal > NIA_CAUSAL_BOTTOM_RIGHT || !(scale > 0.f) ||
+      scale == INFINITY)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (num_seqs == 0 || max_q_len == 0) return NIA_OK;
+  if (!out || !q || !q_start || !q_len || !context_lens) return NIA_ERR_INVALID_ARGUMENT;
+  if (max_blocks_per_seq > 0 && (!k_cache || !v_cache || !block_tables))
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (dtype != NIA_DTYPE_BF16 || !supported_head_dim(head_dim)) return NIA_ERR_UNSUPPORTED;
+  if (block_size <= 0 || block_size > 64 || (block_size & (block_size - 1)))
+    return NIA_ERR_UNSUPPORTED;
+  if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride) ||
+      (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
+    return NIA_ERR_MISALIGNED;
+  PrefillParams p{};
+  p.o = (bf16_t*)out;
+  p.o_tok = out_tok_stride;
+  p.o_head = out_head_stride;
+  p.q = (const bf16_t*)q;
+  p.q_tok = q_tok_stride;
+  p.q_head = q_head_stride;
+  p.k = (const bf16_t*)k_cache;
+  p.v = (const bf16_t*)v_cache;
+  p.q_start = q_start;
+  p.q_len = q_len;
+  p.ctx_len = context_lens;
+  p.block_tables = block_tables;
+  p.bt_stride = bt_stride;
+  p.max_blocks = max_blocks_per_seq;
+  p.num_blocks = num_blocks;
+  p.bs_log2 = __builtin_ctz((unsigned)block_size);
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.num_m_blocks = (max_q_len + kBlockM - 1) / kBlockM;
+  p.causal = causal;
+  p.scale_log2 = scale * kLog2e;
+  return launch_prefill<true>(p, head_dim, num_seqs, (hipStream_t)stream);
+}

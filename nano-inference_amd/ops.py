@@ -1,0 +1,356 @@
+"""Tensor-level wrappers of the gfx950 attention kernels.
+
+Each function validates shapes, dtypes and devices on the host (raising
+ValueError, as the reference layers do for bad configurations,
+src/nano_inference/layers/attention.py:105-116), then calls one C-ABI entry
+point of libnia_attn.so on the current HIP stream.  A nonzero status raises
+``NiaError`` (a RuntimeError).  Nothing here computes attention itself.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import CAUSAL_BOTTOM_RIGHT, CAUSAL_NONE, CAUSAL_TOP_LEFT  # noqa: F401
+
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+
+
+def _dtype_code(t: torch.Tensor, allowed=(torch.bfloat16, torch.float32)) -> int:
+    if t.dtype not in allowed:
+        raise ValueError(f"unsupported dtype {t.dtype}; expected one of {allowed}")
+    return _DTYPES[t.dtype]
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError(
+                f"attention kernels run on the GPU only; got a tensor on {t.device}"
+            )
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _last_contig(name: str, t: torch.Tensor) -> None:
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must have a contiguous last dimension")
+
+
+def _default_scale(head_dim: int, scale: Optional[float]) -> float:
+    # The reference divides the scores by sqrt(head_dim) (attention.py:27).
+    return 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
+
+
+# ---------------------------------------------------------------------------------
+# KV-cache write
+# ---------------------------------------------------------------------------------
+
+
+def kv_write(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Scatter new K/V rows into one layer's paged cache, in place and bit-exact.
+
+    Same effect as the loop at src/nano_inference/layers/attention.py:267-278:
+    for every token t with ``slot = slot_mapping[t] >= 0``,
+    ``k_cache[slot // BS, :, slot % BS, :] = k[t]`` (and likewise for v).
+
+    k, v: (..., H_kv, D) - leading dims are flattened to tokens in the order of
+    ``slot_mapping.reshape(-1)``; k_cache, v_cache: [num_blocks, H_kv, BS, D].
+    """
+    dev = _require_gpu(k, v, k_cache, v_cache, slot_mapping)
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, head_dim]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache layer slices must be contiguous")
+    nb, hkv, bs, d = k_cache.shape
+    if k.shape[-2:] != (hkv, d) or v.shape[-2:] != (hkv, d):
+        raise ValueError(f"k/v trailing shape must be ({hkv}, {d}), got {tuple(k.shape)}")
+    if not (k.dtype == v.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("k, v and the caches must share one dtype")
+    if slot_mapping.dtype != torch.int64:
+        raise ValueError("slot_mapping must be int64 (the context builder's dtype)")
+    dt = _dtype_code(k)
+    k2 = k.reshape(-1, hkv, d)
+    v2 = v.reshape(-1, hkv, d)
+    _last_contig("k", k2)
+    _last_contig("v", v2)
+    slots = slot_mapping.reshape(-1).contiguous()
+    if slots.numel() != k2.shape[0]:
+        raise ValueError(f"{slots.numel()} slots for {k2.shape[0]} tokens")
+    lib = _lib.load()
+    st = lib.nia_kv_write(
+        k2.data_ptr(), k2.stride(0), k2.stride(1),
+        v2.data_ptr(), v2.stride(0), v2.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(),
+        k2.shape[0], hkv, d, bs, nb, dt, _stream(dev),
+    )
+    _lib.check("nia_kv_write", st)
+
+
+# ---------------------------------------------------------------------------------
+# Paged decode
+# ---------------------------------------------------------------------------------
+
+
+def decode_workspace_bytes(batch: int, num_heads: int, max_blocks: int, block_size: int,
+                           head_dim: int) -> int:
+    return int(
+        _lib.load().nia_paged_decode_workspace_size(batch, num_heads, max_blocks, block_size,
+                                                    head_dim)
+    )
+
+
+def paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """One query token per sequence against its paged keys.
+
+    Same result as the decode branch of src/nano_inference/layers/attention.py:285-332
+    for S_step = 1.  q: (B, H, D) or (B, 1, H, D); k_cache/v_cache: one layer,
+    [num_blocks, H_kv, BS, D]; block_tables: (B, max_blocks) int32;
+    context_lens: (B,) int64.  Returns (B, H, D) (or q's 4-D shape).
+    """
+    dev = _require_gpu(q, k_cache, v_cache, block_tables, context_lens)
+    squeeze = q.dim() == 4
+    if squeeze:
+        if q.shape[1] != 1:
+            raise ValueError("paged_decode takes one query token per sequence")
+        q3 = q[:, 0]
+    elif q.dim() == 3:
+        q3 = q
+    else:
+        raise ValueError(f"q must be (B, H, D) or (B, 1, H, D), got {tuple(q.shape)}")
+    b, h, d = q3.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, head_dim]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache layer slices must be contiguous")
+    nb, hkv, bs, dc = k_cache.shape
+    if dc != d:
+        raise ValueError(f"head_dim mismatch: q {d}, cache {dc}")
+    if h % hkv != 0:
+        raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
+    if not (q3.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("q and the caches must share one dtype")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise ValueError("block_tables must be (B, max_blocks) int32")
+    if context_lens.dtype != torch.int64 or context_lens.shape != (b,):
+        raise ValueError("context_lens must be (B,) int64")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    context_lens = context_lens.contiguous()
+    dt = _dtype_code(q3)
+    _last_contig("q", q3)
+    if out is None:
+        out3 = torch.empty((b, h, d), dtype=q3.dtype, device=dev)
+    else:
+        out3 = out[:, 0] if out.dim() == 4 else out
+        if out3.shape != (b, h, d) or out3.dtype != q3.dtype:
+            raise ValueError("out must match q's shape and dtype")
+        _last_contig("out", out3)
+    max_blocks = block_tables.shape[1]
+    need = decode_workspace_bytes(b, h, max_blocks, bs, d)
+    ws_ptr, ws_bytes = 0, 0
+    if need > 0:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    lib = _lib.load()
+    st = lib.nia_paged_decode(
+        out3.data_ptr(), out3.stride(0), out3.stride(1),
+        q3.data_ptr(), q3.stride(0), q3.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        block_tables.data_ptr(), block_tables.stride(0), max_blocks, context_lens.data_ptr(),
+        b, h, hkv, d, bs, nb, _default_scale(d, scale), ws_ptr, ws_bytes, dt, _stream(dev),
+    )
+    _lib.check("nia_paged_decode", st)
+    if out is not None:
+        return out
+    return out3.unsqueeze(1) if squeeze else out3
+
+
+# ---------------------------------------------------------------------------------
+# Prefill (contiguous K/V) and varlen
+# ---------------------------------------------------------------------------------
+
+
+def _i32(name: str, t: torch.Tensor, n: int) -> torch.Tensor:
+    if t.dim() != 1 or t.shape[0] != n:
+        raise ValueError(f"{name} must be ({n},)")
+    return t.to(torch.int32).contiguous()
+
+
+def prefill(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_start: torch.Tensor,
+    q_len: torch.Tensor,
+    k_start: torch.Tensor,
+    k_len: torch.Tensor,
+    max_q_len: int,
+    causal: int = CAUSAL_TOP_LEFT,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Varlen attention over contiguous K/V rows (nia_prefill).
+
+    q/out: (Tq, H, D); k/v: (Tk, H_kv, D), each with a contiguous last dim.
+    Sequence s owns query rows q_start[s] .. + q_len[s] and key rows
+    k_start[s] .. + k_len[s].  ``causal`` is CAUSAL_NONE / CAUSAL_TOP_LEFT /
+    CAUSAL_BOTTOM_RIGHT (see include/nia_attn.h).
+    """
+    dev = _require_gpu(q, k, v, q_start, q_len, k_start, k_len)
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
+        raise ValueError("q must be (Tq, H, D) and k, v (Tk, H_kv, D)")
+    _, h, d = q.shape
+    hkv = k.shape[1]
+    if k.shape[2] != d:
+        raise ValueError("head_dim mismatch between q and k/v")
+    if h % hkv != 0:
+        raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k and v must share one dtype")
+    dt = _dtype_code(q, (torch.bfloat16,))
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _last_contig(name, t)
+    n = q_start.shape[0]
+    qs, ql, ks, kl = (_i32(nm, t, n) for nm, t in
+                      (("q_start", q_start), ("q_len", q_len), ("k_start", k_start),
+                       ("k_len", k_len)))
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    _last_contig("out", out)
+    lib = _lib.load()
+    st = lib.nia_prefill(
+        out.data_ptr(), out.stride(0), out.stride(1),
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        qs.data_ptr(), ql.data_ptr(), ks.data_ptr(), kl.data_ptr(),
+        n, int(max_q_len), h, hkv, d, _default_scale(d, scale), int(causal), dt, _stream(dev),
+    )
+    _lib.check("nia_prefill", st)
+    return out
+
+
+def varlen_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: Optional[torch.Tensor] = None,
+    max_seqlen_q: Optional[int] = None,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Packed varlen attention with cu_seqlens (vision tower: causal=False).
+
+    Chunk i owns rows cu_seqlens[i] .. cu_seqlens[i+1]; causal=True aligns the
+    mask top-left (equal q/k lengths in the prefill case).  ``max_seqlen_q``
+    sizes the launch grid; when omitted it is read back from the device.
+    """
+    if cu_seqlens_k is None:
+        cu_seqlens_k = cu_seqlens_q
+    cq = cu_seqlens_q.to(torch.int32)
+    ck = cu_seqlens_k.to(torch.int32)
+    lq = cq[1:] - cq[:-1]
+    lk = ck[1:] - ck[:-1]
+    if max_seqlen_q is None:
+        max_seqlen_q = int(lq.max().item()) if lq.numel() else 0
+    return prefill(q, k, v, cq[:-1], lq, ck[:-1], lk, max_seqlen_q,
+                   CAUSAL_TOP_LEFT if causal else CAUSAL_NONE, scale, out)
+
+
+# ---------------------------------------------------------------------------------
+# Chunked prefill over the paged cache
+# ---------------------------------------------------------------------------------
+
+
+def prefill_paged(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    q_start: torch.Tensor,
+    q_len: torch.Tensor,
+    context_lens: torch.Tensor,
+    max_q_len: int,
+    causal: int = CAUSAL_BOTTOM_RIGHT,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Query chunks against their paged keys (nia_prefill_paged).
+
+    q/out: (Tq, H, D).  Sequence s has q_len[s] query rows starting at token
+    q_start[s], sitting at absolute positions context_lens[s] - q_len[s] + j,
+    and reads keys [0, context_lens[s]) through block_tables (B, max_blocks) int32.
+    """
+    dev = _require_gpu(q, k_cache, v_cache, block_tables, q_start, q_len, context_lens)
+    if q.dim() != 3:
+        raise ValueError("q must be (Tq, H, D)")
+    _, h, d = q.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, head_dim]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache layer slices must be contiguous")
+    nb, hkv, bs, dc = k_cache.shape
+    if dc != d:
+        raise ValueError("head_dim mismatch between q and the cache")
+    if h % hkv != 0:
+        raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
+    if not (q.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("q and the caches must share one dtype")
+    dt = _dtype_code(q, (torch.bfloat16,))
+    _last_contig("q", q)
+    n = q_start.shape[0]
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != n:
+        raise ValueError("block_tables must be (B, max_blocks) int32")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    if context_lens.dtype != torch.int64 or context_lens.shape != (n,):
+        raise ValueError("context_lens must be (B,) int64")
+    qs, ql = _i32("q_start", q_start, n), _i32("q_len", q_len, n)
+    context_lens = context_lens.contiguous()
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    elif out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    _last_contig("out", out)
+    lib = _lib.load()
+    st = lib.nia_prefill_paged(
+        out.data_ptr(), out.stride(0), out.stride(1),
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k_cache.data_ptr(), v_cache.data_ptr(),
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1],
+        qs.data_ptr(), ql.data_ptr(), context_lens.data_ptr(),
+        n, int(max_q_len), h, hkv, d, bs, nb, _default_scale(d, scale), int(causal), dt,
+        _stream(dev),
+    )
+    _lib.check("nia_prefill_paged", st)
+    return out

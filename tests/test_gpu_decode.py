@@ -1,0 +1,167 @@
+"""Paged decode kernel vs the float64 oracle, plus closed forms and invariants.
+
+Oracle: oracle.textbook (softmax(q K^T / sqrt(D)) V per sequence over keys
+[0, context_len), head h -> KV head h // G), the mathematics of
+src/nano_inference/layers/attention.py:285-332 and :12-50.
+Bars: bf16 max-abs 2e-2 / mean-abs 2e-3, fp32 max-abs 1e-5.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nano_inference_amd import ops, workloads
+from oracle import textbook as tb
+from tests.tolerances import assert_attn_close
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_decode(c: workloads.DecodeCase, layer: int = 0, seqs=None,
+                  scale=None) -> np.ndarray:
+    """Float64 oracle, streaming one sequence's blocks at a time from the GPU."""
+    b, h, d = c.q.shape
+    hkv = c.num_kv_heads
+    g = h // hkv
+    q = c.q.double().cpu().numpy()
+    out = np.zeros((b, h, d))
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    for i in range(b) if seqs is None else seqs:
+        L = c.lens[i]
+        ids = torch.tensor(c.tables_list[i], device=c.k_cache.device)
+        kb = c.k_cache[layer][ids].double().cpu().numpy()  # (n, H_kv, BS, D)
+        vb = c.v_cache[layer][ids].double().cpu().numpy()
+        kk = kb.transpose(1, 0, 2, 3).reshape(hkv, -1, d)[:, :L]
+        vv = vb.transpose(1, 0, 2, 3).reshape(hkv, -1, d)[:, :L]
+        for hk in range(hkv):
+            out[i, hk * g:(hk + 1) * g] = tb.attend(q[i, hk * g:(hk + 1) * g], kk[hk], vv[hk], scale)
+    return out
+
+
+def run_step(c: workloads.DecodeCase, layer: int = 0) -> torch.Tensor:
+    ops.kv_write(c.k_new, c.v_new, c.k_cache[layer], c.v_cache[layer], c.slot_mapping)
+    out = ops.paged_decode(c.q, c.k_cache[layer], c.v_cache[layer], c.block_tables,
+                           c.context_lens)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_small(dtype):
+    """4 sequences, 16/8 heads, contexts 17/64/200/511, 128-block pool."""
+    c = workloads.decode_small("cuda", dtype)
+    out = run_step(c)
+    assert_attn_close(out, oracle_decode(c), dtype, f"decode_small {dtype}")
+
+
+def test_decode_qwen3_8b_full_batch():
+    """64 sequences, 32/8 heads, contexts U[512, 8192], 40k-block shuffled pool."""
+    c = workloads.decode_qwen3_8b("cuda")
+    out = run_step(c)
+    assert_attn_close(out, oracle_decode(c), torch.bfloat16, "decode_qwen3_8b")
+
+
+def test_decode_vl_group_of_seven():
+    """32 sequences, 28/4 heads (7 query heads per KV head), contexts U[1024, 6144]."""
+    c = workloads.decode_vl("cuda")
+    out = run_step(c)
+    assert_attn_close(out, oracle_decode(c), torch.bfloat16, "decode_vl")
+
+
+@pytest.mark.parametrize("group", [1, 2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_block_boundaries(group, dtype):
+    lens = [1, 2, 15, 16, 17, 31, 32, 33, 511, 512, 513, 1025]
+    hkv = 2
+    c = workloads.make_decode(len(lens), hkv * group, hkv, 128, lens, 512, 16, dtype, "cuda",
+                              seed=40 + group)
+    out = run_step(c)
+    assert_attn_close(out, oracle_decode(c), dtype, f"boundaries G={group}")
+
+
+def test_zero_context_gives_zeros():
+    c = workloads.make_decode(3, 8, 2, 128, [5, 40, 600], 64, 16, torch.bfloat16, "cuda", 77)
+    ctx = torch.tensor([0, 40, 0], dtype=torch.int64, device="cuda")
+    out = ops.paged_decode(c.q, c.k_cache[0], c.v_cache[0], c.block_tables, ctx)
+    torch.cuda.synchronize()
+    assert out[0].eq(0).all() and out[2].eq(0).all()
+    assert_attn_close(out[1], oracle_decode(c, seqs=[1])[1], torch.bfloat16, "ctx 40")
+
+
+def test_block_table_permutation_is_bit_invariant():
+    """Moving every block to another physical id (and updating the table) changes nothing."""
+    c = workloads.make_decode(6, 16, 4, 128, [100, 700, 1600, 33, 512, 2049], 1024, 16,
+                              torch.bfloat16, "cuda", 91)
+    out1 = run_step(c)
+    perm = torch.randperm(1024, generator=torch.Generator().manual_seed(1)).cuda()
+    k2 = torch.empty_like(c.k_cache[0])
+    v2 = torch.empty_like(c.v_cache[0])
+    k2[perm] = c.k_cache[0]
+    v2[perm] = c.v_cache[0]
+    bt2 = perm[c.block_tables.long()].to(torch.int32)
+    out2 = ops.paged_decode(c.q, k2, v2, bt2, c.context_lens)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+
+
+def test_garbage_past_context_and_in_padding_blocks_is_ignored():
+    """NaN in slots past L (same block) and in block 0 (padded table entries)."""
+    c = workloads.make_decode(4, 8, 2, 128, [20, 33, 48, 100], 64, 16, torch.bfloat16, "cuda", 5)
+    out1 = run_step(c)
+    kc, vc = c.k_cache[0], c.v_cache[0]
+    used = {b for t in c.tables_list for b in t}
+    for i, L in enumerate(c.lens):
+        last = c.tables_list[i][(L - 1) // 16]
+        kc[last, :, (L - 1) % 16 + 1:] = float("nan")
+        vc[last, :, (L - 1) % 16 + 1:] = float("inf")
+    if 0 not in used:
+        kc[0] = float("nan")
+        vc[0] = float("nan")
+    out2 = ops.paged_decode(c.q, kc, vc, c.block_tables, c.context_lens)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+
+
+def test_closed_forms():
+    """L = 1 gives v_0 exactly; equal keys give mean(V); constant V gives that constant."""
+    hkv, g, d = 2, 4, 128
+    c = workloads.make_decode(3, hkv * g, hkv, d, [1, 300, 300], 64, 16, torch.float32, "cuda", 8)
+    kc, vc = c.k_cache[0], c.v_cache[0]
+    # sequence 1: identical keys
+    ids1 = c.tables_list[1]
+    kc[ids1] = kc[ids1[0], :, :1].clone()  # broadcast key 0 to every slot of its blocks
+    # sequence 2: constant values per head
+    ids2 = c.tables_list[2]
+    vc[ids2] = torch.arange(hkv, device="cuda", dtype=torch.float32).view(1, hkv, 1, 1) + 0.25
+    out = ops.paged_decode(c.q, kc, vc, c.block_tables, c.context_lens)
+    torch.cuda.synchronize()
+    v0 = vc[c.tables_list[0][0], :, 0]  # (H_kv, D)
+    assert torch.equal(out[0], v0.repeat_interleave(g, 0))
+    vv = vc[torch.tensor(ids1, device="cuda")].permute(1, 0, 2, 3).reshape(hkv, -1, d)[:, :300]
+    torch.testing.assert_close(out[1], vv.mean(1).repeat_interleave(g, 0), atol=1e-5, rtol=0)
+    exp2 = (torch.arange(hkv, device="cuda", dtype=torch.float32) + 0.25).repeat_interleave(g)
+    torch.testing.assert_close(out[2], exp2.view(-1, 1).expand(-1, d), atol=1e-6, rtol=0)
+
+
+def test_gqa_equals_mha_with_repeated_kv():
+    g, hkv = 4, 2
+    c = workloads.make_decode(5, hkv * g, hkv, 128, [40, 90, 600, 1, 257], 128, 16,
+                              torch.bfloat16, "cuda", 13)
+    out_gqa = run_step(c)
+    k_mha = c.k_cache[0].repeat_interleave(g, dim=1).contiguous()
+    v_mha = c.v_cache[0].repeat_interleave(g, dim=1).contiguous()
+    out_mha = ops.paged_decode(c.q, k_mha, v_mha, c.block_tables, c.context_lens)
+    torch.cuda.synchronize()
+    # Not bit-equal: a group shares its lazy-rescale decisions across its heads.
+    assert_attn_close(out_gqa, out_mha.double().cpu().numpy(), torch.bfloat16, "GQA vs MHA")
+
+
+def test_four_dim_query_and_explicit_scale():
+    c = workloads.decode_small("cuda", torch.float32)
+    run_step(c)
+    out4 = ops.paged_decode(c.q.unsqueeze(1), c.k_cache[0], c.v_cache[0], c.block_tables,
+                            c.context_lens, scale=0.05)
+    torch.cuda.synchronize()
+    assert out4.shape == (4, 1, 16, 128)
+    assert_attn_close(out4[:, 0], oracle_decode(c, scale=0.05), torch.float32, "scale 0.05")
