@@ -1,0 +1,324 @@
+"""Benchmark of the gfx950 attention path (one JSON line on stdout).
+
+Workload (``config.workload``): paged decode at the Qwen3-8B layout - 64
+sequences, 32 query / 8 KV heads, head_dim 128, contexts uniform in
+[512, 8192], block size 16, a shuffled 40,000-block pool, bf16.  One step is
+one attention layer's decode pass: write the 64 new K/V tokens into the cache
+(nia_kv_write), then paged decode attention (nia_paged_decode).  Steps rotate
+over 4 cache layers so that no step finds the previous step's KV in the
+256 MB last-level cache.
+
+value = algorithmic HBM bytes of a step / step time, in GB/s.  The bytes are
+  decode:  sum_i L_i * H_kv * D * 2 * 2 (K and V) + 2 * B * H * D * 2 (q, out)
+           + 4 * sum_i ceil(L_i / 16) (block table) + 8 * B (context_lens)
+  write:   4 * B * H_kv * D * 2 (read k, v; write both caches) + 8 * B (slots)
+The JSON line also carries the decode kernel's roofline (HBM, 8 TB/s peak),
+causal prefill TFLOP/s against bf16 MFMA peak (2.5 PFLOP/s dense), the other
+synthetic workloads, and the reference's CPU attention timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       python bench.py --profile-decode N   (only N decode steps plus a 1 GiB copy,
+                                             for rocprofv3 counter runs)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+DECODE_LAYERS = 4
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_calls(torch, fn, iters: int, warmup: int = 3) -> float:
+    """Average milliseconds per call of fn (events on the current stream)."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    a, b = _events(torch)
+    a.record()
+    for i in range(iters):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def per_call_ms(torch, fn, iters: int) -> float:
+    """Mean of per-call event timings (each call bracketed by its own events)."""
+    pairs = []
+    for i in range(iters):
+        a, b = _events(torch)
+        a.record()
+        fn(i)
+        b.record()
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / iters
+
+
+def read_traffic(workload: str):
+    """Per-launch HBM bytes of the decode kernels from a committed counter summary."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            m = re.match(r"\s*(\w+)\s*[:=]\s*([0-9.eE+-]+)", line)
+            if m:
+                vals[m.group(1)] = float(m.group(2))
+    if "hbm_bytes_per_launch" in vals:
+        return vals["hbm_bytes_per_launch"]
+    return None
+
+
+def bench_decode(torch, ops, workloads, steps: int, warmup: int):
+    c = workloads.decode_qwen3_8b("cuda", layers=DECODE_LAYERS)
+    b, h, d = c.q.shape
+    out = torch.empty_like(c.q)
+    ws = torch.empty(ops.decode_workspace_bytes(b, h, c.block_tables.shape[1], 16, d),
+                     dtype=torch.uint8, device="cuda")
+
+    def write(i):
+        L = i % DECODE_LAYERS
+        ops.kv_write(c.k_new, c.v_new, c.k_cache[L], c.v_cache[L], c.slot_mapping)
+
+    def decode(i):
+        L = i % DECODE_LAYERS
+        ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens,
+                         out=out, workspace=ws)
+
+    def step(i):
+        write(i)
+        decode(i)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    a, e = _events(torch)
+    a.record()
+    for i in range(steps):
+        step(i)
+    e.record()
+    torch.cuda.synchronize()
+    ms_step = a.elapsed_time(e) / steps
+    iters = max(steps, 20)
+    dec_ms = per_call_ms(torch, decode, iters)
+    wr_ms = per_call_ms(torch, write, iters)
+    return c, ms_step, dec_ms, wr_ms
+
+
+def bench_prefill(torch, ops, workloads):
+    res = {}
+    c = workloads.prefill_qwen3_8b("cuda")
+    cu = c.cu_seqlens
+    qs, ql = cu[:-1].contiguous(), (cu[1:] - cu[:-1]).contiguous()
+    out = torch.empty_like(c.q)
+    mq = max(c.lens)
+
+    def run(_):
+        ops.prefill(c.q, c.k, c.v, qs, ql, qs, ql, mq, ops.CAUSAL_TOP_LEFT, out=out)
+
+    ms = time_calls(torch, run, 20)
+    tf = c.flops() / (ms * 1e-3) / 1e12
+    res["prefill_qwen3_8b"] = dict(ms=round(ms, 4), tflops=round(tf, 1),
+                                   frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                                   seqlens=c.lens, flops=c.flops())
+    ch = workloads.chunked_qwen3_8b("cuda")
+    outc = torch.empty_like(ch.q)
+
+    def runc(_):
+        ops.prefill_paged(ch.q, ch.k_cache, ch.v_cache, ch.block_tables, ch.q_start, ch.q_len,
+                          ch.context_lens, ch.chunk, out=outc)
+
+    ms = time_calls(torch, runc, 20)
+    tf = ch.flops() / (ms * 1e-3) / 1e12
+    res["chunked_qwen3_8b"] = dict(ms=round(ms, 4), tflops=round(tf, 1),
+                                   frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), prior=ch.prior,
+                                   chunk=ch.chunk, flops=ch.flops())
+    for window in (False, True):
+        v = workloads.vision_vl("cuda", window=window)
+        cuv = v.cu_seqlens
+        vs, vl = cuv[:-1].contiguous(), (cuv[1:] - cuv[:-1]).contiguous()
+        outv = torch.empty_like(v.q)
+        mv = max(v.lens)
+
+        def runv(_):
+            ops.prefill(v.q, v.k, v.v, vs, vl, vs, vl, mv, ops.CAUSAL_NONE, out=outv)
+
+        ms = time_calls(torch, runv, 30)
+        tf = v.flops() / (ms * 1e-3) / 1e12
+        res[v.name] = dict(ms=round(ms, 4), tflops=round(tf, 1),
+                           frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), chunks=len(v.lens),
+                           flops=v.flops())
+    return res
+
+
+def bench_decode_vl(torch, ops, workloads):
+    c = workloads.decode_vl("cuda", layers=DECODE_LAYERS)
+    out = torch.empty_like(c.q)
+
+    def decode(i):
+        L = i % DECODE_LAYERS
+        ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens,
+                         out=out)
+
+    for i in range(5):
+        decode(i)
+    ms = per_call_ms(torch, decode, 40)
+    gbps = c.decode_bytes() / (ms * 1e-3) / 1e9
+    return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
+                bytes=c.decode_bytes())
+
+
+def cpu_baseline(torch, workloads, budget_s: float = 20.0):
+    """The reference's decode attention (op-for-op CPU restatement), fp32, on a sample.
+
+    Sample: the first 8 sequences of the decode workload (same lengths, same
+    head layout), the reference's write loop + padded gather + repeat_interleave
+    + materialised softmax, repeated until about ``budget_s`` seconds have passed.
+    """
+    from oracle import reference_attention as ref
+
+    n = max(1, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(n)
+    lens = workloads.uniform_lengths(64, 512, 8192, 2002)[:8]
+    pool = sum(math.ceil(L / 16) for L in lens) + 64
+    c = workloads.make_decode(8, 32, 8, 128, lens, pool, 16, torch.float32, "cpu", 2002)
+    kc, vc = c.k_cache[0], c.v_cache[0]
+    mask = ref.decode_context_mask(c.context_lens)
+
+    def once():
+        ref.paged_attention(c.q.unsqueeze(1), c.k_new, c.v_new, kc, vc, c.slot_mapping,
+                            c.block_tables, c.context_lens, mask, is_prefill=False)
+
+    once()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    byts = c.decode_bytes() + c.write_bytes()
+    return dict(value=round(byts / med / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(),
+                kind="port",
+                sample=(f"reference decode attention (write loop, padded gather, "
+                        f"repeat_interleave, fp32 softmax) on the first 8 sequences of the "
+                        f"workload (contexts {lens}), fp32, median of {len(times)} runs, "
+                        f"{med * 1e3:.1f} ms per run; bytes counted at fp32 element size"))
+
+
+def profile_decode(torch, ops, workloads, n: int) -> None:
+    """Minimal run for counter collection: a 1 GiB copy (calibration) and n decodes."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    c = workloads.decode_qwen3_8b("cuda", layers=DECODE_LAYERS)
+    for i in range(n):
+        L = i % DECODE_LAYERS
+        ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(copy_bytes=1 << 30, decode_bytes=c.decode_bytes(),
+                          kv_bytes=c.kv_bytes())), flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--profile-decode", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the attention path has no multi-GPU leg", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from nano_inference_amd import ops, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    if args.profile_decode:
+        profile_decode(torch, ops, workloads, args.profile_decode)
+        return 0
+
+    c, ms_step, dec_ms, wr_ms = bench_decode(torch, ops, workloads, args.steps, args.warmup)
+    step_bytes = c.decode_bytes() + c.write_bytes()
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    dec_gbps = c.decode_bytes() / (dec_ms * 1e-3) / 1e9
+    extra = {"decode_vl": bench_decode_vl(torch, ops, workloads)}
+    extra.update(bench_prefill(torch, ops, workloads))
+    pf = extra["prefill_qwen3_8b"]
+    extra["kv_write_qwen3_8b"] = dict(us=round(wr_ms * 1e3, 2),
+                                      gbps=round(c.write_bytes() / (wr_ms * 1e-3) / 1e9, 1))
+    line = {
+        "metric": "decode attn HBM GB/s (% of peak) + prefill attn TFLOP/s (% bf16 MFMA peak)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/k/v and KV pool, seeded",
+        "config": {
+            "workload": "paged decode, Qwen3-8B layout: B=64, 32/8 heads, D=128, "
+                        "contexts U[512,8192], block 16, shuffled 40k-block pool; "
+                        "step = KV write of 64 tokens + paged decode (one layer)",
+            "batch": c.batch, "num_heads": c.num_heads, "num_kv_heads": c.num_kv_heads,
+            "head_dim": c.head_dim, "block_size": 16, "pool_blocks": 40000,
+            "context_tokens": sum(c.lens), "step_bytes": step_bytes,
+        },
+        "roofline": {
+            "kernel": "paged decode (partial + combine)",
+            "bound": "hbm",
+            "achieved": round(dec_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": read_traffic("decode_qwen3_8b"),
+            "algorithmic_bytes": c.decode_bytes(),
+            "us_per_launch": round(dec_ms * 1e3, 2),
+        },
+        "prefill": {
+            "workload": "causal varlen prefill, Qwen3-8B layout, 8 seqs U[256,4096]",
+            "tflops": pf["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": pf["frac"], "ms": pf["ms"],
+        },
+        "extra": extra,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(torch, workloads, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
