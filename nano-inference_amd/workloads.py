@@ -209,7 +209,8 @@ class ChunkedCase:
 
 
 def chunked_qwen3_8b(device="cuda", dtype=torch.bfloat16, seed: int = 3103, n: int = 8,
-                     chunk: int = 512, prior: Optional[List[int]] = None) -> ChunkedCase:
+                     chunk: int = 512, prior: Optional[List[int]] = None,
+                     num_heads: int = 32, num_kv_heads: int = 8) -> ChunkedCase:
     prior = uniform_lengths(n, 0, 8192, seed) if prior is None else list(prior)
     bs = 16
     ctx = [p + chunk for p in prior]
@@ -223,9 +224,9 @@ def chunked_qwen3_8b(device="cuda", dtype=torch.bfloat16, seed: int = 3103, n: i
         tables[i, :nb] = torch.tensor(perm[off:off + nb], dtype=torch.int32)
         tl.append(perm[off:off + nb])
         off += nb
-    shape = (pool, 8, bs, 128)
+    shape = (pool, num_kv_heads, bs, 128)
     return ChunkedCase(
-        q=_randn((n * chunk, 32, 128), dtype, device, seed + 2),
+        q=_randn((n * chunk, num_heads, 128), dtype, device, seed + 2),
         k_cache=_randn(shape, dtype, device, seed + 3),
         v_cache=_randn(shape, dtype, device, seed + 4),
         block_tables=tables.to(device),

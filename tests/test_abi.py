@@ -1,0 +1,77 @@
+"""The C-ABI library loads and exports every symbol include/nia_attn.h declares (CPU).
+
+No kernel is launched: only entry points that return before touching the GPU
+(argument validation, sizes, strings) are called.
+"""
+import ctypes
+import os
+import re
+
+from nano_inference_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "nia_attn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nia_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_and_error_strings():
+    lib = _lib.load()
+    assert lib.nia_abi_version() == _lib.ABI_VERSION
+    for code in range(6):
+        assert lib.nia_error_string(code)
+    assert lib.nia_error_string(0) == b"ok"
+    assert lib.nia_error_string(99) == b"unknown status"
+
+
+def test_validation_returns_codes_without_launching():
+    lib = _lib.load()
+    # negative token count
+    assert lib.nia_kv_write(None, 0, 0, None, 0, 0, None, None, None, -1, 8, 128, 16, 10,
+                            0, None) == _lib.ERR_INVALID_ARGUMENT
+    # zero tokens: nothing to do
+    assert lib.nia_kv_write(None, 0, 0, None, 0, 0, None, None, None, 0, 8, 128, 16, 10,
+                            0, None) == _lib.OK
+    # unsupported dtype
+    assert lib.nia_kv_write(None, 0, 0, None, 0, 0, None, None, None, 1, 8, 128, 16, 10,
+                            7, None) == _lib.ERR_UNSUPPORTED
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # decode: heads not divisible
+    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 6, 4, 128, 16, 10, 0.1,
+                                None, 0, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    # decode: unsupported head_dim
+    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 72, 16, 10, 0.1,
+                                None, 0, 0, None) == _lib.ERR_UNSUPPORTED
+    # decode: workspace too small for 2 partitions
+    assert lib.nia_paged_decode(p, 128, 128, p, 1024, 128, p, p, p, 64, 64, p, 2, 8, 4, 128, 16,
+                                100, 0.1, None, 0, 0, None) == _lib.ERR_WORKSPACE
+    # prefill: fp32 has no MFMA kernel
+    assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.1,
+                           1, 1, None) == _lib.ERR_UNSUPPORTED
+    # prefill: bad causal mode, non-positive scale
+    assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.1,
+                           5, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.0,
+                           1, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    # paged prefill: block size not a power of two
+    assert lib.nia_prefill_paged(p, 8, 8, p, 8, 8, p, p, p, 4, 4, p, p, p, 1, 4, 2, 2, 128, 12,
+                                 10, 0.1, 2, 0, None) == _lib.ERR_UNSUPPORTED
+
+
+def test_workspace_size():
+    lib = _lib.load()
+    assert lib.nia_paged_decode_workspace_size(64, 32, 32, 16, 128) == 0  # one partition
+    assert lib.nia_paged_decode_workspace_size(64, 32, 512, 16, 128) == 64 * 32 * 16 * 130 * 4
