@@ -19,6 +19,7 @@ synthetic workloads, and the reference's CPU attention timed on this host.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
        python bench.py --profile-decode N   (only N decode steps plus a 1 GiB copy,
                                              for rocprofv3 counter runs)
+       python bench.py --profile-prefill N  (only N causal prefill launches)
 """
 from __future__ import annotations
 
@@ -90,7 +91,7 @@ def bench_decode(torch, ops, workloads, steps: int, warmup: int):
     c = workloads.decode_qwen3_8b("cuda", layers=DECODE_LAYERS)
     b, h, d = c.q.shape
     out = torch.empty_like(c.q)
-    ws = torch.empty(ops.decode_workspace_bytes(b, h, c.block_tables.shape[1], 16, d),
+    ws = torch.zeros(ops.decode_workspace_bytes(b, h, c.block_tables.shape[1], 16, d),
                      dtype=torch.uint8, device="cuda")
 
     def write(i):
@@ -241,6 +242,18 @@ def profile_decode(torch, ops, workloads, n: int) -> None:
                           kv_bytes=c.kv_bytes())), flush=True)
 
 
+def profile_prefill(torch, ops, workloads, n: int) -> None:
+    """Minimal run for counter collection: n causal prefill launches."""
+    c = workloads.prefill_qwen3_8b("cuda")
+    cu = c.cu_seqlens
+    qs, ql = cu[:-1].contiguous(), (cu[1:] - cu[:-1]).contiguous()
+    out = torch.empty_like(c.q)
+    for _ in range(n):
+        ops.prefill(c.q, c.k, c.v, qs, ql, qs, ql, max(c.lens), ops.CAUSAL_TOP_LEFT, out=out)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(flops=c.flops())), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +262,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--profile-decode", type=int, default=0)
+    ap.add_argument("--profile-prefill", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -264,6 +278,9 @@ def main() -> int:
         return 1
     if args.profile_decode:
         profile_decode(torch, ops, workloads, args.profile_decode)
+        return 0
+    if args.profile_prefill:
+        profile_prefill(torch, ops, workloads, args.profile_prefill)
         return 0
 
     c, ms_step, dec_ms, wr_ms = bench_decode(torch, ops, workloads, args.steps, args.warmup)

@@ -89,7 +89,12 @@ int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
  * produce zeros.  Block ids outside [0, num_blocks) are skipped.
  *   q, out       [batch, num_heads, head_dim] with element strides (batch, head).
  *   block_tables [batch, bt_stride] int32, the first max_blocks_per_seq columns used.
- *   workspace    >= nia_paged_decode_workspace_size(...) bytes of device memory.
+ *   workspace    >= nia_paged_decode_workspace_size(...) bytes of device memory,
+ *                256-byte aligned.  Its leading bytes hold work counters: the
+ *                whole workspace must be zero before its first use; every call
+ *                that completes leaves the counters at zero again, so one
+ *                workspace serves any number of calls issued one after another
+ *                (calls that overlap in time need workspaces of their own).
  * Supported: head_dim 128; block_size 16; num_heads / num_kv_heads in 1..8;
  * dtype bf16 (fp32 softmax and accumulation) or f32.
  */

@@ -136,7 +136,6 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         self.k_norm = RMSNorm(hd) if use_qk_norm else None
         self.rotary = RotaryEmbedding(head_dim=hd, base=rope_base)
         self.layer_idx: Optional[int] = None
-        self._decode_ws: Optional[torch.Tensor] = None
 
     def _apply_rotary(self, q, k, position_ids, metadata=None) -> Tuple[torch.Tensor, torch.Tensor]:
         return self.rotary(q, k, position_ids)
@@ -200,13 +199,7 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
             ctx = metadata.context_lens
             if s == 1:
                 # 2b. Decode: gather + GQA + mask + softmax in one kernel (:285-332).
-                need = ops.decode_workspace_bytes(b, self.num_heads, bt.shape[1],
-                                                  k_cache.shape[2], self.head_dim)
-                if need and (self._decode_ws is None or self._decode_ws.numel() < need
-                             or self._decode_ws.device != x.device):
-                    self._decode_ws = torch.empty(need, dtype=torch.uint8, device=x.device)
-                attn = ops.paged_decode(q[:, 0], k_cache, v_cache, bt, ctx,
-                                        workspace=self._decode_ws)
+                attn = ops.paged_decode(q[:, 0], k_cache, v_cache, bt, ctx)
             else:
                 # 2c. Several new tokens on top of cached context: chunked prefill.
                 dev = x.device

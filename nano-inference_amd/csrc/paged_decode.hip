@@ -26,6 +26,11 @@
 //   rows merge by shuffles, waves through LDS, partitions in the combine kernel.
 // Algorithmic HBM bytes per sequence: 2 * L * H_kv * D * s (K and V) plus q, out,
 // 4 * ceil(L / BS) table bytes and the 8-byte context length.
+#include <map>
+#include <mutex>
+#include <type_traits>
+#include <utility>
+
 #include "common.h"
 
 namespace {
@@ -106,6 +111,58 @@ struct Elem<float> {
   }
   static NIA_DEVICE float from_f32(float x) { return x; }
 };
+
+// Merge the per-wave softmax states of a workgroup through LDS and store either
+// the final output (single-partition sequence) or the partition's partial
+// (m, l, un-normalised o) for the combine kernel.  On entry the lanes with
+// row == 0 hold o[g][col * EL .. +EL) and every lane holds the wave's m, l.
+template <typename T, int D, int G, int EL>
+NIA_DEVICE void merge_waves_and_store(const DecodeParams& p, const float (&o)[G][EL],
+                                      const float (&m)[G], const float (&l)[G], int row,
+                                      int col, int wave, int b, int hk, int part, int nparts) {
+  __shared__ float sm_o[kDecodeWaves][G][D];
+  __shared__ float sm_m[kDecodeWaves][G];
+  __shared__ float sm_l[kDecodeWaves][G];
+  if (row == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < EL; ++e) sm_o[wave][g][col * EL + e] = o[g][e];
+      if (col == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads) {
+    const int g = idx / D;
+    const int d = idx - g * D;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) mt = fmaxf(mt, sm_m[w][g]);
+    float lt = 0.f, ot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float mw = sm_m[w][g];
+      const float wt = (mw == -INFINITY) ? 0.f : fast_exp2(mw - mt);
+      lt = fmaf(sm_l[w][g], wt, lt);
+      ot = fmaf(sm_o[w][g][d], wt, ot);
+    }
+    const int h = hk * G + g;
+    if (nparts == 1) {
+      T* out = reinterpret_cast<T*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h;
+      out[d] = (T)(lt > 0.f ? ot / lt : 0.f);
+    } else {
+      const int64_t slot = ((int64_t)b * p.num_heads + h) * p.max_parts + part;
+      p.ws_o[slot * D + d] = ot;
+      if (d == 0) {
+        p.ws_ml[slot * 2 + 0] = mt;
+        p.ws_ml[slot * 2 + 1] = lt;
+      }
+    }
+  }
+}
 
 template <typename T, int D, int G, int BS, int PART_BLOCKS>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_partial_kernel(DecodeParams p) {
@@ -276,49 +333,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_partial_kernel(De
     }
   }
 
-  // ---- merge the waves through LDS ---------------------------------------------------
-  __shared__ float sm_o[kDecodeWaves][G][D];
-  __shared__ float sm_m[kDecodeWaves][G];
-  __shared__ float sm_l[kDecodeWaves][G];
-  if (row == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < EL; ++e) sm_o[wave][g][col * EL + e] = o[g][e];
-      if (col == 0) {
-        sm_m[wave][g] = m[g];
-        sm_l[wave][g] = l[g];
-      }
-    }
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
-    float mt = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) mt = fmaxf(mt, sm_m[w][g]);
-    float lt = 0.f, ot = 0.f;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) {
-      const float mw = sm_m[w][g];
-      const float wt = (mw == -INFINITY) ? 0.f : fast_exp2(mw - mt);
-      lt = fmaf(sm_l[w][g], wt, lt);
-      ot = fmaf(sm_o[w][g][d], wt, ot);
-    }
-    const int h = hk * G + g;
-    if (nparts == 1) {
-      T* out = reinterpret_cast<T*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h;
-      out[d] = E::from_f32(lt > 0.f ? ot / lt : 0.f);
-    } else {
-      const int64_t slot = ((int64_t)b * p.num_heads + h) * p.max_parts + part;
-      p.ws_o[slot * D + d] = ot;
-      if (d == 0) {
-        p.ws_ml[slot * 2 + 0] = mt;
-        p.ws_ml[slot * 2 + 1] = lt;
-      }
-    }
-  }
+  merge_waves_and_store<T, D, G>(p, o, m, l, row, col, wave, b, hk, part, nparts);
 }
 
 // Merge the partition partials of one (sequence, head); one thread per dim.
@@ -350,16 +365,477 @@ __global__ __launch_bounds__(D) void paged_decode_combine_kernel(DecodeParams p)
   out[d] = E::from_f32(lt > 0.f ? ot / lt : 0.f);
 }
 
-constexpr int kPartBlocks = 32;  // 512 tokens per workgroup at block size 16
+// Wave-wide max (every lane receives the maximum over all 64 lanes).
+NIA_DEVICE float wave_max(float x) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
+  return x;
+}
+
+NIA_DEVICE float wave_sum(float x) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
+  return x;
+}
+
+// bf16 decode, head_dim 128, block size 16 (the serving layout).
+//
+// Two lane layouts share one wave:
+//   K layout: 8 lanes per token.  Wave-wide load j of a block reads token
+//     (l / 8) + 8 (j / 2), dims 16 (l % 8) + 8 (j % 2) .. +7, so a q . k dot
+//     product is 8 bf16 dot2 per lane and a 3-step DPP sum over 8 lanes, and
+//     each lane owns 2 tokens per block for the softmax.
+//   V layout: 16 lanes per token, fully coalesced: load i reads token 4i + l/16,
+//     dims 8 (l % 16) .. +7.
+// Blocks are processed in pairs (A, B).  For each K-layout token the softmax
+// weights of blocks A and B are packed into one bf16 pair and moved to the
+// V-layout lanes with ds_bpermute; there P.V is v_dot2_f32_bf16 over the
+// (A, B) token pair, with V's two tokens interleaved by v_perm.  The running
+// max is uniform over the wave (raised lazily by more than 2^8), so row and
+// lane partials add without rescaling.  Per 4 KB block-head this is about
+// 64 dot2 (QK) + 64 dot2 (PV) + 24 DPP + ~40 softmax/convert VALU operations.
+// A wave has one pair (16 KB) of loads in flight at a time; latency is hidden
+// across the 4 waves per SIMD that the register budget (<= 128 VGPRs at
+// G <= 4) allows.
+template <int G>
+struct DecodeState {
+  uint32_t qw[G][8];
+  float o[G][8];
+  float l[G];
+  float m[G];
+};
+
+// Issue the 8 wave-wide loads of one block-head (4 K in the K layout, 4 V in the
+// V layout); an index past the partition or an invalid block id gives zeros.
+NIA_DEVICE bool decode_load_block(const DecodeParams& p, const bf16_t* kcache,
+                                  const bf16_t* vcache, int my_bt, int jx, int blk_begin,
+                                  int blk_end, int hk, int lane, uint4 (&kr)[4],
+                                  uint4 (&vr)[4]) {
+  constexpr int BS = 16, D = 128;
+  const int ktok = lane >> 3, kc = lane & 7;
+  const int blk = jx < blk_end ? __builtin_amdgcn_readlane(my_bt, jx - blk_begin) : -1;
+  const bool ok = blk >= 0 && (int64_t)blk < p.num_blocks;
+  if (ok) {
+    const int64_t base = ((int64_t)blk * p.num_kv_heads + hk) * (BS * D);
+    const uint4* kp = reinterpret_cast<const uint4*>(kcache + base);
+    const uint4* vp = reinterpret_cast<const uint4*>(vcache + base);
+    kr[0] = kp[ktok * 16 + 2 * kc];
+    kr[1] = kp[ktok * 16 + 2 * kc + 1];
+    kr[2] = kp[(ktok + 8) * 16 + 2 * kc];
+    kr[3] = kp[(ktok + 8) * 16 + 2 * kc + 1];
+    vr[0] = vp[lane];
+    vr[1] = vp[64 + lane];
+    vr[2] = vp[128 + lane];
+    vr[3] = vp[192 + lane];
+  } else {
+    kr[0] = kr[1] = kr[2] = kr[3] = make_uint4(0, 0, 0, 0);
+    vr[0] = vr[1] = vr[2] = vr[3] = make_uint4(0, 0, 0, 0);
+  }
+  return ok;
+}
+
+// Zero the V rows of one 16-token block (V layout) that lie past the context
+// or belong to an invalid block id.
+NIA_DEVICE void zero_invalid_v(uint4 (&v)[4], bool ok, int tok0, int ctx, int vrow) {
+  if (ok && tok0 + 16 <= ctx) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bool valid = ok && (tok0 + 4 * i + vrow) < ctx;
+    v[i].x = valid ? v[i].x : 0u;
+    v[i].y = valid ? v[i].y : 0u;
+    v[i].z = valid ? v[i].z : 0u;
+    v[i].w = valid ? v[i].w : 0u;
+  }
+}
+
+template <int G>
+NIA_DEVICE void decode_compute_pair(const DecodeParams& p, DecodeState<G>& st,
+                                    const uint4 (&kA)[4], const uint4 (&kB)[4],
+                                    uint4 (&vA)[4], uint4 (&vB)[4], bool okA, bool okB,
+                                    int jb, int ctx, int lane) {
+  constexpr int BS = 16;
+  const int ktok = lane >> 3;
+  const int vrow = lane >> 4;
+  // ---- scores (K layout) ----------------------------------------------------------------
+  float xs[2][2][G];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const bool valid = (x ? okB : okA) && ((jb + x) * BS + 8 * sl + ktok) < ctx;
+      const uint4 k0 = x ? kB[2 * sl] : kA[2 * sl];
+      const uint4 k1 = x ? kB[2 * sl + 1] : kA[2 * sl + 1];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float s = dot2_bf16(st.qw[g][0], k0.x, 0.f);
+        s = dot2_bf16(st.qw[g][1], k0.y, s);
+        s = dot2_bf16(st.qw[g][2], k0.z, s);
+        s = dot2_bf16(st.qw[g][3], k0.w, s);
+        s = dot2_bf16(st.qw[g][4], k1.x, s);
+        s = dot2_bf16(st.qw[g][5], k1.y, s);
+        s = dot2_bf16(st.qw[g][6], k1.z, s);
+        s = dot2_bf16(st.qw[g][7], k1.w, s);
+        s = group_sum<8>(s);
+        xs[x][sl][g] = valid ? s * p.scale_log2 : -INFINITY;
+      }
+    }
+  }
+  // ---- lazy wave-uniform running max -------------------------------------------------------
+  float bm[G];
+  bool need = false;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    bm[g] = fmaxf(fmaxf(xs[0][0][g], xs[0][1][g]), fmaxf(xs[1][0][g], xs[1][1][g]));
+    need |= bm[g] > st.m[g] + kLazyRescale;
+  }
+  if (wave_any(need)) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mn = fmaxf(st.m[g], wave_max(bm[g]));
+      const float corr = (st.m[g] == -INFINITY) ? 0.f : fast_exp2(st.m[g] - mn);
+      st.m[g] = mn;
+      st.l[g] *= corr;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) st.o[g][e] *= corr;
+    }
+  }
+  // ---- weights, packed (A, B) per token ----------------------------------------------------
+  uint32_t pp[2][G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float msub = (st.m[g] == -INFINITY) ? 0.f : st.m[g];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const float pa = fast_exp2(xs[0][sl][g] - msub);
+      const float pb2 = fast_exp2(xs[1][sl][g] - msub);
+      st.l[g] += pa + pb2;
+      pp[sl][g] = pack_bf16x2(pa, pb2);
+    }
+  }
+  // Slots past the context (or in an invalid block) hold stale data of any
+  // value: zero their V so that 0 * garbage cannot produce NaN.
+  zero_invalid_v(vA, okA, jb * BS, ctx, vrow);
+  zero_invalid_v(vB, okB, (jb + 1) * BS, ctx, vrow);
+  // ---- O += P V (V layout) -----------------------------------------------------------------
+  // ds_bpermute byte addresses: V-layout load i reads the K-layout lane that
+  // owns its token, 8 * (4 (i % 2) + l / 16), from slot i / 2.
+  const int bp_addr0 = (8 * vrow) * 4;
+  const int bp_addr1 = (8 * (4 + vrow)) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t pv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      pv[g] = (uint32_t)__builtin_amdgcn_ds_bpermute((i & 1) ? bp_addr1 : bp_addr0,
+                                                     (int)pp[i >> 1][g]);
+    const uint32_t va[4] = {vA[i].x, vA[i].y, vA[i].z, vA[i].w};
+    const uint32_t vb[4] = {vB[i].x, vB[i].y, vB[i].z, vB[i].w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);
+      const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        st.o[g][2 * w] = dot2_bf16(pv[g], lo, st.o[g][2 * w]);
+        st.o[g][2 * w + 1] = dot2_bf16(pv[g], hi, st.o[g][2 * w + 1]);
+      }
+    }
+  }
+}
+
+// A sequence's blocks are split into ceil(blocks / PART_BLOCKS) partitions of
+// near-equal size (so a 600-token context is 19 + 19 blocks, not 32 + 6).
+NIA_DEVICE void decode_partition(int ctx_blocks, int part_blocks, int part, int& nparts,
+                                 int& begin, int& end) {
+  nparts = (ctx_blocks + part_blocks - 1) / part_blocks;
+  begin = (int)(((int64_t)part * ctx_blocks) / nparts);
+  end = (int)(((int64_t)(part + 1) * ctx_blocks) / nparts);
+}
+
+// One work item of the bf16 decode: partition `part` (blocks [blk_begin,
+// blk_end)) of sequence b and KV head hk, all G query heads of the group.  The
+// workgroup's 4 waves take the partition's block pairs round-robin; their
+// states merge through LDS and leave as the final output (single-partition
+// sequence) or as a partial for the partition merge.
+template <int G, int PART_BLOCKS>
+NIA_DEVICE void decode_bf16_item(const DecodeParams& p, int b, int hk, int part, int nparts,
+                                 int blk_begin, int blk_end, int ctx) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int kc = lane & 7;     // K layout: 16-dim chunk
+  const int vrow = lane >> 4;  // V layout: token within a 4-token load
+  const int vc = lane & 15;    // V layout: 8-dim chunk
+
+  const bf16_t* kcache = reinterpret_cast<const bf16_t*>(p.k_cache);
+  const bf16_t* vcache = reinterpret_cast<const bf16_t*>(p.v_cache);
+  const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
+
+  // The partition's block-table slice, one entry per lane, read once so that
+  // no K/V load waits behind a table load inside the loop.
+  static_assert(PART_BLOCKS <= kWave, "one table entry per lane");
+  const int my_bt = (lane < blk_end - blk_begin) ? bt[blk_begin + lane] : -1;
+
+  DecodeState<G> st;
+  {
+    const bf16_t* qb = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)b * p.q_b;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint4* qp = reinterpret_cast<const uint4*>(qb + (int64_t)(hk * G + g) * p.q_h + 16 * kc);
+      const uint4 a = qp[0], c = qp[1];
+      st.qw[g][0] = a.x; st.qw[g][1] = a.y; st.qw[g][2] = a.z; st.qw[g][3] = a.w;
+      st.qw[g][4] = c.x; st.qw[g][5] = c.y; st.qw[g][6] = c.z; st.qw[g][7] = c.w;
+      st.m[g] = -INFINITY;
+      st.l[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) st.o[g][e] = 0.f;
+    }
+  }
+
+  {
+    constexpr int kStep = 2 * kDecodeWaves;
+    for (int jb = blk_begin + 2 * wave; jb < blk_end; jb += kStep) {
+      uint4 kA[4], vA[4], kB[4], vB[4];
+      const bool okA =
+          decode_load_block(p, kcache, vcache, my_bt, jb, blk_begin, blk_end, hk, lane, kA, vA);
+      const bool okB = decode_load_block(p, kcache, vcache, my_bt, jb + 1, blk_begin, blk_end,
+                                         hk, lane, kB, vB);
+      decode_compute_pair<G>(p, st, kA, kB, vA, vB, okA, okB, jb, ctx, lane);
+    }
+  }
+
+  // ---- wave totals: rows of the V layout add (shared max); l counted 8x ----------------
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      st.o[g][e] += __shfl_xor(st.o[g][e], 16, kWave);
+      st.o[g][e] += __shfl_xor(st.o[g][e], 32, kWave);
+    }
+    st.l[g] = wave_sum(st.l[g]) * 0.125f;
+  }
+  merge_waves_and_store<bf16_t, D, G>(p, st.o, st.m, st.l, vrow, vc, wave, b, hk, part, nparts);
+}
+
+// Zero output rows of a sequence with no keys (all G heads of KV head hk).
+template <int G>
+NIA_DEVICE void decode_zero_output(const DecodeParams& p, int b, int hk) {
+  constexpr int D = 128;
+  bf16_t* ob = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b;
+  for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads)
+    ob[(int64_t)(hk * G + idx / D) * p.out_h + idx % D] = (bf16_t)0.f;
+}
+
+// Grid-per-partition variant: grid (max partitions, KV heads, sequences); the
+// partials are merged by paged_decode_combine_kernel.  Used when the batch is
+// too large for the persistent kernel's LDS index.
+template <int G, int PART_BLOCKS>
+__global__ __launch_bounds__(kDecodeThreads) void paged_decode_bf16_kernel(DecodeParams p) {
+  constexpr int BS = 16;
+  const int part = blockIdx.x;
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  int64_t ctx64 = p.context_lens[b];
+  const int64_t cap = (int64_t)p.max_blocks * BS;
+  if (ctx64 > cap) ctx64 = cap;
+  const int ctx = ctx64 > 0 ? (int)ctx64 : 0;
+  int nparts, blk_begin, blk_end;
+  decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
+  if (part >= nparts) {
+    // Whole workgroup leaves together.  A sequence without keys gets zeros from
+    // its first partition.
+    if (part == 0 && ctx == 0) decode_zero_output<G>(p, b, hk);
+    return;
+  }
+  decode_bf16_item<G, PART_BLOCKS>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
+}
+
+// Largest batch the persistent kernel indexes in LDS (prefix sums of the
+// per-sequence partition counts).
+constexpr int kPersistentMaxBatch = 4096;
+
+// Persistent variant: a grid of as many workgroups as the chip holds at once.
+// Work items are (sequence, partition, KV head) in that order, numbered on the
+// device from context_lens; workgroups take them from an atomic ticket counter
+// (the next ticket is requested while the current item runs), so the grid
+// never carries empty workgroups and a short item is followed at once by the
+// next.  Partials go to paged_decode_combine_kernel, launched after this one.
+// The two counters live at the start of the workspace: they must be zero
+// before the first call, and the last workgroup to leave returns them to zero.
+template <int G, int PART_BLOCKS>
+__global__ __launch_bounds__(kDecodeThreads)
+__attribute__((amdgpu_waves_per_eu(G <= 4 ? 3 : 2))) void paged_decode_bf16_persistent_kernel(
+    DecodeParams p, int batch, int* counters) {
+  constexpr int BS = 16;
+  __shared__ int s_prefix[kPersistentMaxBatch + 1];
+  __shared__ int s_scan[kDecodeThreads];
+  __shared__ int s_ticket[2];
+  const int tid = threadIdx.x;
+  const int64_t cap = (int64_t)p.max_blocks * BS;
+
+  // First ticket goes out before the index is built.
+  if (tid == 0) s_ticket[0] = atomicAdd(&counters[0], 1);
+
+  // ---- partitions per sequence and their exclusive prefix sums ------------------------
+  // Thread t owns sequences [t * kPer, t * kPer + kPer): one pass for its sum,
+  // a workgroup scan, a second pass to write the prefixes.
+  constexpr int kPer = (kPersistentMaxBatch + kDecodeThreads - 1) / kDecodeThreads;
+  auto parts_of = [&](int bi) -> int {
+    int64_t c = p.context_lens[bi];
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    const int blocks = (int)((c + BS - 1) / BS);
+    return blocks > 0 ? (blocks + PART_BLOCKS - 1) / PART_BLOCKS : 1;  // 1 zero-fill item
+  };
+  const int b0 = tid * kPer;
+  const int b1 = min(b0 + kPer, batch);
+  int run = 0;
+  for (int bi = b0; bi < b1; ++bi) run += parts_of(bi);
+  s_scan[tid] = run;
+  __syncthreads();
+  for (int off = 1; off < kDecodeThreads; off <<= 1) {
+    const int v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  run = tid > 0 ? s_scan[tid - 1] : 0;
+  for (int bi = b0; bi < b1; ++bi) {
+    s_prefix[bi] = run;
+    run += parts_of(bi);
+  }
+  if (tid == 0) s_prefix[batch] = s_scan[kDecodeThreads - 1];
+  __syncthreads();
+  const int total = s_prefix[batch] * p.num_kv_heads;
+
+  // ---- item loop ------------------------------------------------------------------------
+  for (int it = 0;; ++it) {
+    const int item = s_ticket[it & 1];
+    if (item >= total) break;
+    // Ask for the next ticket now; its value is only needed at the end of this
+    // item, so the request's latency hides behind the item's loads.
+    int next = 0;
+    if (tid == 0) next = atomicAdd(&counters[0], 1);
+    const int sp = item / p.num_kv_heads;
+    const int hk = item - sp * p.num_kv_heads;
+    int lo = 0, hi = batch;  // largest b with s_prefix[b] <= sp
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_prefix[mid] <= sp) lo = mid; else hi = mid;
+    }
+    const int b = lo;
+    const int part = sp - s_prefix[b];
+    int64_t c = p.context_lens[b];
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    const int ctx = (int)c;
+    if (ctx == 0) {
+      decode_zero_output<G>(p, b, hk);
+    } else {
+      int nparts, blk_begin, blk_end;
+      decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
+      decode_bf16_item<G, PART_BLOCKS>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
+    }
+    if (tid == 0) s_ticket[(it + 1) & 1] = next;
+    __syncthreads();  // next ticket visible; LDS of this item free
+  }
+  // ---- leave: the last workgroup out returns the counters to zero -------------------------
+  // Every workgroup increments the exit count only after its final (failed)
+  // ticket request returned, so when the count completes no request is pending.
+  if (tid == 0) {
+    const int left = atomicAdd(&counters[1], 1);
+    if (left == (int)gridDim.x - 1) {
+      atomicExch(&counters[0], 0);
+      atomicExch(&counters[1], 0);
+    }
+  }
+}
+
+constexpr int kPartBlocks = 32;  // 512 tokens per work item at block size 16
+
+// Workspace layout: [work counters (256 B)][m, l per partial][o per partial].
+constexpr size_t kCounterBytes = 256;
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+int32_t decode_max_parts(int32_t max_blocks_per_seq) {
+  return (max_blocks_per_seq + kPartBlocks - 1) / kPartBlocks;
+}
+
+// Workgroups per CU the persistent kernel reaches, cached per (device, G).
+std::mutex g_occ_mutex;
+std::map<std::pair<int, int>, int> g_occ;
+
+template <int G>
+int persistent_grid(int device, int upper) {
+  int per_cu = 0, cus = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_occ_mutex);
+    auto it = g_occ.find({device, G});
+    if (it != g_occ.end()) {
+      per_cu = it->second & 0xffff;
+      cus = it->second >> 16;
+    }
+  }
+  if (per_cu == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return -1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, paged_decode_bf16_persistent_kernel<G, kPartBlocks>, kDecodeThreads, 0) !=
+        hipSuccess)
+      return -1;
+    if (per_cu < 1) per_cu = 1;
+    std::lock_guard<std::mutex> lock(g_occ_mutex);
+    g_occ[{device, G}] = (cus << 16) | per_cu;
+  }
+  // Two workgroups per CU (8 waves, 16 KB of K/V in flight each) measured faster
+  // than the register-limited maximum of three: the extra streams of random
+  // 4 KB block-heads only add contention in the memory system.
+  const int full = cus * (per_cu < 2 ? per_cu : 2);
+  return upper < full ? upper : full;
+}
 
 template <typename T, int D, int BS>
-int launch_decode(const DecodeParams& p, int G, int batch, hipStream_t s) {
+int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStream_t s) {
+  constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
+  if (kBf16 && batch <= kPersistentMaxBatch) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return NIA_ERR_LAUNCH;
+    const int upper = batch * p.num_kv_heads * (p.max_parts > 0 ? p.max_parts : 1);
+    switch (G) {
+#define NIA_CASE(GG)                                                                          \
+  case GG: {                                                                                  \
+    const int grid = persistent_grid<GG>(device, upper);                                      \
+    if (grid < 1) return NIA_ERR_LAUNCH;                                                      \
+    hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocks>), dim3(grid),    \
+                       dim3(kDecodeThreads), 0, s, p, batch, counters);                       \
+    break;                                                                                    \
+  }
+      NIA_CASE(1)
+      NIA_CASE(2)
+      NIA_CASE(3)
+      NIA_CASE(4)
+      NIA_CASE(5)
+      NIA_CASE(6)
+      NIA_CASE(7)
+      NIA_CASE(8)
+#undef NIA_CASE
+      default:
+        return NIA_ERR_UNSUPPORTED;
+    }
+    if (p.max_parts > 1)
+      hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, kPartBlocks>),
+                         dim3(p.num_heads, batch), dim3(D), 0, s, p);
+    return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+  }
   const dim3 grid(p.max_parts, p.num_kv_heads, batch);
   switch (G) {
 #define NIA_CASE(GG)                                                                          \
   case GG:                                                                                    \
-    hipLaunchKernelGGL((paged_decode_partial_kernel<T, D, GG, BS, kPartBlocks>), grid,        \
-                       dim3(kDecodeThreads), 0, s, p);                                        \
+    if constexpr (kBf16)                                                                      \
+      hipLaunchKernelGGL((paged_decode_bf16_kernel<GG, kPartBlocks>), grid,                   \
+                         dim3(kDecodeThreads), 0, s, p);                                      \
+    else                                                                                      \
+      hipLaunchKernelGGL((paged_decode_partial_kernel<T, D, GG, BS, kPartBlocks>), grid,      \
+                         dim3(kDecodeThreads), 0, s, p);                                      \
     break;
     NIA_CASE(1)
     NIA_CASE(2)
@@ -379,20 +855,15 @@ int launch_decode(const DecodeParams& p, int G, int batch, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
-int32_t decode_max_parts(int32_t max_blocks_per_seq) {
-  return (max_blocks_per_seq + kPartBlocks - 1) / kPartBlocks;
-}
-
 }  // namespace
 
 extern "C" size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_heads,
                                                   int32_t max_blocks_per_seq,
                                                   int32_t block_size, int32_t head_dim) {
   (void)block_size;
-  if (batch <= 0 || num_heads <= 0 || max_blocks_per_seq <= 0 || head_dim <= 0) return 0;
-  const size_t parts = (size_t)decode_max_parts(max_blocks_per_seq);
-  if (parts <= 1) return 0;
-  return (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
+  if (batch <= 0 || num_heads <= 0 || max_blocks_per_seq < 0 || head_dim <= 0) return 0;
+  const size_t parts = (size_t)decode_max_parts(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1);
+  return kCounterBytes + (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
 }
 
 extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_stride,
@@ -440,11 +911,15 @@ extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t
   p.max_parts = decode_max_parts(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1);
   const size_t need = nia_paged_decode_workspace_size(batch, num_heads, max_blocks_per_seq,
                                                       block_size, head_dim);
-  if (need > 0 && (!workspace || workspace_bytes < need)) return NIA_ERR_WORKSPACE;
-  p.ws_o = reinterpret_cast<float*>(workspace);
-  p.ws_ml = need > 0 ? p.ws_o + (size_t)batch * num_heads * p.max_parts * head_dim : nullptr;
+  if (!workspace || workspace_bytes < need) return NIA_ERR_WORKSPACE;
+  if ((uintptr_t)workspace % 256) return NIA_ERR_MISALIGNED;
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  int* counters = reinterpret_cast<int*>(ws);
+  p.ws_ml = reinterpret_cast<float*>(ws + kCounterBytes);
+  p.ws_o = p.ws_ml + (size_t)batch * num_heads * p.max_parts * 2;
 
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NIA_DTYPE_BF16) return launch_decode<bf16_t, 128, 16>(p, G, batch, s);
-  return launch_decode<float, 128, 16>(p, G, batch, s);
+  if (dtype == NIA_DTYPE_BF16)
+    return launch_decode<bf16_t, 128, 16>(p, G, batch, counters, s);
+  return launch_decode<float, 128, 16>(p, G, batch, counters, s);
 }

@@ -115,6 +115,25 @@ def decode_workspace_bytes(batch: int, num_heads: int, max_blocks: int, block_si
     )
 
 
+_DECODE_WS: dict = {}
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A zero-initialised decode workspace of at least ``nbytes``, cached per device.
+
+    The decode kernel keeps its work counters at the start of the workspace and
+    returns them to zero at the end of every call, so a workspace must be zero
+    once, before its first use, and then serves any number of calls made one
+    after another on one stream.
+    """
+    key = torch.device(device)
+    ws = _DECODE_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=key)
+        _DECODE_WS[key] = ws
+    return ws
+
+
 def paged_decode(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -131,6 +150,8 @@ def paged_decode(
     for S_step = 1.  q: (B, H, D) or (B, 1, H, D); k_cache/v_cache: one layer,
     [num_blocks, H_kv, BS, D]; block_tables: (B, max_blocks) int32;
     context_lens: (B,) int64.  Returns (B, H, D) (or q's 4-D shape).
+    ``workspace`` (optional, uint8) must have been zero before its first use
+    (see ``decode_workspace``); by default a cached per-device one is used.
     """
     dev = _require_gpu(q, k_cache, v_cache, block_tables, context_lens)
     squeeze = q.dim() == 4
@@ -172,11 +193,12 @@ def paged_decode(
         _last_contig("out", out3)
     max_blocks = block_tables.shape[1]
     need = decode_workspace_bytes(b, h, max_blocks, bs, d)
-    ws_ptr, ws_bytes = 0, 0
-    if need > 0:
-        if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    if workspace is None:
+        workspace = decode_workspace(dev, need)
+    ws_bytes = workspace.numel() * workspace.element_size()
+    if ws_bytes < need:
+        raise ValueError(f"decode workspace of {ws_bytes} bytes, {need} needed")
+    ws_ptr = workspace.data_ptr()
     lib = _lib.load()
     st = lib.nia_paged_decode(
         out3.data_ptr(), out3.stride(0), out3.stride(1),

@@ -73,5 +73,9 @@ def test_validation_returns_codes_without_launching():
 
 def test_workspace_size():
     lib = _lib.load()
-    assert lib.nia_paged_decode_workspace_size(64, 32, 32, 16, 128) == 0  # one partition
-    assert lib.nia_paged_decode_workspace_size(64, 32, 512, 16, 128) == 64 * 32 * 16 * 130 * 4
+    # 256 B of work counters, then (m, l) and the partial output per
+    # (sequence, head, partition).
+    counters = 256
+    assert lib.nia_paged_decode_workspace_size(64, 32, 32, 16, 128) == counters + 64 * 32 * 130 * 4
+    assert lib.nia_paged_decode_workspace_size(64, 32, 512, 16, 128) == \
+        counters + 64 * 32 * 16 * 130 * 4
