@@ -26,6 +26,8 @@
 // raised when a tile's max exceeds it by more than 2^8 (lazy rescale).
 // Causal tiles above the diagonal are never visited; tiles crossing it are masked.
 // MFMA work per (query, key) pair: 4 * D flops (QK^T and PV).
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -59,9 +61,40 @@ struct PrefillParams {
   int32_t num_kv_heads;
   int32_t group;
   int32_t num_m_blocks;
+  int32_t num_seqs;
+  int32_t groups_per_xcd;  // ceil(num_seqs * num_kv_heads / kXcds)
   int32_t causal;
   float scale_log2;
 };
+
+// Workgroup -> (sequence, head, m-block) mapping of the 1-D prefill grid.
+//
+// The hardware hands workgroups to the 8 XCDs round-robin (id % 8), and each
+// XCD has its own L2.  A (sequence, KV head) "group" owns the K/V rows that all
+// its m-blocks and its G query heads read, so every group is pinned to one XCD
+// (group % 8 == id % 8) and its K/V is fetched into one L2 only.  Inside an XCD
+// the workgroups go out m-block-major from the bottom of the causal triangle,
+// so the longest rows of every group start first and the short ones fill the
+// tail.  Ids that map past the real work (ragged sequences, uneven groups per
+// XCD) return false.
+constexpr int kXcds = 8;
+
+NIA_DEVICE bool prefill_map(const PrefillParams& p, int& seq, int& h, int& mb) {
+  const int id = blockIdx.x;
+  const int x = id % kXcds;
+  const int t = id / kXcds;
+  const int per_z = p.groups_per_xcd * p.group;
+  const int z = t / per_z;
+  const int rem = t - z * per_z;
+  const int j = rem / p.group;
+  const int g = rem - j * p.group;
+  const int gid = x + kXcds * j;
+  if (z >= p.num_m_blocks || gid >= p.num_seqs * p.num_kv_heads) return false;
+  seq = gid / p.num_kv_heads;
+  h = (gid - seq * p.num_kv_heads) * p.group + g;
+  mb = p.num_m_blocks - 1 - z;
+  return true;
+}
 
 // XOR swizzle of the 4-key groups inside a transposed-V row (row = head dim d).
 NIA_DEVICE int vt_swz(int d) { return (d ^ (d >> 3)) & 15; }
@@ -81,9 +114,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
   __shared__ __attribute__((aligned(16))) uint8_t k_lds[kBlockN * K_PITCH];
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[DP * VT_PITCH];
 
-  const int seq = blockIdx.z;
-  const int h = blockIdx.y;
-  const int mb = p.num_m_blocks - 1 - (int)blockIdx.x;  // long rows first
+  int seq, h, mb;
+  if (!prefill_map(p, seq, h, mb)) return;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -330,9 +362,302 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
   }
 }
 
+// ---------------------------------------------------------------------------------
+// head_dim 128 kernel: K/V tiles stream global -> LDS by direct DMA
+// (global_load_lds_dwordx4), double-buffered, and the V^T MFMA operand is read
+// with ds_read_b64_tr_b16 from a row-major V tile, so no VGPR staging, no
+// ds_write and no transpose work remains on the VALU.
+//
+// LDS tile layout (K and V alike): 64 rows x 256 B, 16-byte chunk c of row r
+// stored at chunk position c ^ f(r), f(r) = 4 (r & 3) + ((r & 15) >> 2).  A row
+// is exactly one sweep of the LDS banks, so banks are set by the chunk position
+// alone; f maps the 16 rows of a group to 16 distinct XOR masks (K operand
+// reads: 16 rows of one chunk column) and moves the 4-chunk span of each of 4
+// consecutive rows to a different quarter of the row (transposed V reads: 4
+// rows x 4 chunks per 32 lanes), so both read patterns are conflict-free.  A
+// DMA instruction writes lane i's 16 B at base + 16 i, so the swizzle is
+// applied by choosing which global chunk each lane fetches.
+// Wave w fills rows 16w .. 16w + 15 of each tile: for block sizes >= 16 these
+// rows lie in one KV block, whose id is one scalar load per wave and tile.
+// Rows past the context are clamped to the last key (finite data, masked to
+// -inf in S, so they contribute exactly zero).
+// ---------------------------------------------------------------------------------
+
+constexpr int kTileRowBytes = 256;                 // 128 bf16
+constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
+
+NIA_DEVICE int tile_swz(int r) { return ((r & 3) << 2) | ((r & 15) >> 2); }
+
+NIA_DEVICE void lds_dma16(const void* g, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+                                   0, 0);
+}
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element (j % 4)
+// of the 4-element rows addressed by lanes 4r + j / 4, r = 0..3 (a 16x4 <-> 4x16
+// transpose of 16-bit elements).
+NIA_DEVICE s16x4_t lds_read_tr16(const uint8_t* addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)addr);
+}
+
+template <bool PAGED>
+__global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(PrefillParams p) {
+  constexpr int D = 128;
+  constexpr int DK = D / 16;
+  constexpr int DT = D / 32;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2][kTileBytes];  // [stage][K, V]
+
+  int seq, h, mb;
+  if (!prefill_map(p, seq, h, mb)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = uniform(tid / kWave);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+
+  const int qlen = p.q_len[seq];
+  const int m0 = mb * kBlockM;
+  if (m0 >= qlen) return;
+  int klen;
+  int64_t kstart = 0;
+  if constexpr (PAGED) {
+    int64_t c = p.ctx_len[seq];
+    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    klen = (int)c;
+  } else {
+    klen = p.k_len[seq];
+    kstart = p.k_start[seq];
+  }
+  const int64_t qstart = p.q_start[seq];
+  const int hk = h / p.group;
+  const bool causal = p.causal != NIA_CAUSAL_NONE;
+  const int q_pos0 = p.causal == NIA_CAUSAL_BOTTOM_RIGHT ? klen - qlen : 0;
+  int n_end = klen;
+  if (causal) n_end = min(klen, q_pos0 + min(m0 + kBlockM, qlen));
+  if (n_end < 0) n_end = 0;
+
+  const int r0 = m0 + wave * 32;
+  const int qrow = r0 + col;
+  const bool row_ok = qrow < qlen;
+  const int kb = causal ? min(klen, q_pos0 + qrow + 1) : klen;
+  const int wave_kmin = causal ? min(klen, q_pos0 + r0 + 1) : klen;
+  const int wave_kend = r0 < qlen ? (causal ? min(klen, q_pos0 + min(r0 + 32, qlen)) : klen) : 0;
+
+  uint4 qreg[DK];
+  {
+    const bf16_t* qp = p.q + (qstart + (row_ok ? qrow : 0)) * p.q_tok + (int64_t)h * p.q_head;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk)
+      qreg[kk] = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk + 8 * half)
+                        : make_uint4(0, 0, 0, 0);
+  }
+  f32x16_t oacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  // ---- DMA geometry: instruction i of wave w writes rows 16w + 4i + (lane / 16) ----------
+  const int ld_sub = lane >> 4;
+  const int ld_pc = lane & 15;
+  const int32_t* bt = PAGED ? p.block_tables + (int64_t)seq * p.bt_stride : nullptr;
+  const int bs_mask = (1 << p.bs_log2) - 1;
+  // First key row of this wave's 16-row group in tile n0, clamped into the context.
+  auto group_key = [&](int n0) { return min(n0 + 16 * wave, klen - 1); };
+  auto block_of = [&](int n0) __attribute__((always_inline)) -> int {
+    if constexpr (PAGED) {
+      const int b = bt[uniform(group_key(n0) >> p.bs_log2)];
+      return (b < 0 || (int64_t)b >= p.num_blocks) ? -1 : b;
+    } else {
+      return 0;
+    }
+  };
+  // Lane constants of the DMA: row rr[i] of the wave's 16-row group and the
+  // element offset of the swizzled 16-byte chunk it fetches.
+  int rr[4], cc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    rr[i] = 4 * i + ld_sub;
+    cc[i] = 8 * (ld_pc ^ tile_swz(rr[i]));
+  }
+  auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
+    uint8_t* kdst = lds[stage][0] + wave * 16 * kTileRowBytes;
+    uint8_t* vdst = lds[stage][1] + wave * 16 * kTileRowBytes;
+    const int g0 = n0 + 16 * wave;        // first key of the group (uniform)
+    const int gk = min(g0, klen - 1);     // clamped into the context
+    const bool full = g0 + 15 < klen;
+    const bf16_t* kb;
+    const bf16_t* vb;
+    int64_t ks_row, vs_row;               // element stride between key rows
+    if constexpr (PAGED) {
+      // An invalid block id reads block 0 of the KV head: finite data, and the
+      // rows it feeds are masked.
+      const int64_t base_row =
+          ((((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << p.bs_log2) + (gk & bs_mask));
+      kb = p.k + base_row * D;
+      vb = p.v + base_row * D;
+      ks_row = vs_row = D;
+    } else {
+      kb = p.k + (kstart + gk) * p.k_tok + (int64_t)hk * p.k_head;
+      vb = p.v + (kstart + gk) * p.v_tok + (int64_t)hk * p.v_head;
+      ks_row = p.k_tok;
+      vs_row = p.v_tok;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // Rows past the context repeat the last key (masked later).
+      const int dr = full ? rr[i] : min(g0 + rr[i], klen - 1) - gk;
+      lds_dma16(kb + dr * ks_row + cc[i], kdst + i * 1024);
+      lds_dma16(vb + dr * vs_row + cc[i], vdst + i * 1024);
+    }
+  };
+
+  // ---- per-lane LDS read offsets ---------------------------------------------------------
+  // K operand (A of S^T = K Q^T): row 32c + col, chunk 2 kk + half.
+  int k_off[DK];
+#pragma unroll
+  for (int kk = 0; kk < DK; ++kk)
+    k_off[kk] = col * kTileRowBytes + 16 * ((2 * kk + half) ^ tile_swz(col));
+  // V^T operand via transposed reads: 16-lane group g reads rows
+  // 16 kc + 4 (g / 2) + i / 4 (+ 8 for the second read), dims
+  // 32 dt + 16 (g % 2) + 4 (i % 4) .. + 3, i = lane % 16.
+  const int i16 = lane & 15;
+  const int g16 = lane >> 4;
+  const int vr15 = 4 * (g16 >> 1) + (i16 >> 2);  // row & 15 of the first read
+  const int vcd = 2 * (g16 & 1) + ((i16 & 3) >> 1);
+  // The second read is 8 rows lower, so its swizzle uses row & 15 = vr15 + 8.
+  int v_off[DT], v_off2[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    v_off[dt] = vr15 * kTileRowBytes + 16 * ((4 * dt + vcd) ^ tile_swz(vr15)) + 8 * (i16 & 1);
+    v_off2[dt] =
+        (vr15 + 8) * kTileRowBytes + 16 * ((4 * dt + vcd) ^ tile_swz(vr15 + 8)) + 8 * (i16 & 1);
+  }
+
+  auto compute_tile = [&](int n0, int stage) __attribute__((always_inline)) {
+    const uint8_t* kt = lds[stage][0];
+    const uint8_t* vt = lds[stage][1];
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[c][r] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < DK; ++kk) {
+        const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kTileRowBytes + k_off[kk]);
+        sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]), sacc[c], 0,
+            0, 0);
+      }
+    }
+    if (n0 + kBlockN > wave_kmin) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = n0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (key >= kb) sacc[c][r] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float mx2 = mx * p.scale_log2;
+    if (wave_any(mx2 > m_run + kLazyRescaleP)) {
+      const float mn = fmaxf(m_run, mx2);
+      const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
+      m_run = mn;
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+    }
+    const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+    uint4 pb[4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p0 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub));
+          const float p1 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub));
+          l_run += p0 + p1;
+          w[j] = pack_bf16x2(p0, p1);
+        }
+        pb[2 * c + hh] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const s16x4_t lo = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off[dt]);
+        const s16x4_t hi = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off2[dt]);
+        const s16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, pb[kc]), oacc[dt], 0,
+            0, 0);
+      }
+    }
+  };
+
+  // ---- main loop: tile n0 in lds[stage] while tile n0 + 64 streams into the other --------
+  // Unrolled by two so that each stage's LDS offsets are compile-time constants.
+  if (n_end > 0) {
+    int blk_nxt = block_of(0);
+    issue_tile(0, 0, blk_nxt);
+    if (kBlockN < n_end) blk_nxt = block_of(kBlockN);
+    auto step = [&](int n0, auto stage_c) __attribute__((always_inline)) {
+      constexpr int kStage = decltype(stage_c)::value;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (n0 + kBlockN < n_end) {
+        issue_tile(n0 + kBlockN, kStage ^ 1, blk_nxt);
+        if (n0 + 2 * kBlockN < n_end) blk_nxt = block_of(n0 + 2 * kBlockN);
+      }
+      if (n0 < wave_kend) compute_tile(n0, kStage);
+    };
+    for (int n0 = 0; n0 < n_end; n0 += 2 * kBlockN) {
+      step(n0, std::integral_constant<int, 0>());
+      if (n0 + kBlockN < n_end) step(n0 + kBlockN, std::integral_constant<int, 1>());
+    }
+  }
+
+  // ---- epilogue --------------------------------------------------------------------------
+  if (!row_ok) return;
+  const float lt = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  bf16_t* op = p.o + (qstart + qrow) * p.o_tok + (int64_t)h * p.o_head;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * dt + 8 * g + 4 * half;
+      const uint2 val = make_uint2(pack_bf16x2(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv),
+                                   pack_bf16x2(oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv));
+      *reinterpret_cast<uint2*>(op + d) = val;
+    }
+  }
+}
+
 template <bool PAGED>
 int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream_t s) {
-  const dim3 grid(p.num_m_blocks, p.num_heads, num_seqs);
+  const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd * p.group * p.num_m_blocks;
+  if (nwg >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)nwg);
   switch (head_dim) {
     case 64:
       hipLaunchKernelGGL((prefill_kernel<64, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
@@ -344,7 +669,10 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
       hipLaunchKernelGGL((prefill_kernel<96, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
       break;
     case 128:
-      hipLaunchKernelGGL((prefill_kernel<128, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
+      if (!PAGED || p.bs_log2 >= 4)
+        hipLaunchKernelGGL((prefill_d128_kernel<PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL((prefill_kernel<128, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
       break;
     default:
       return NIA_ERR_UNSUPPORTED;
@@ -403,6 +731,8 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;
   p.num_m_blocks = (max_q_len + kBlockM - 1) / kBlockM;
+  p.num_seqs = num_seqs;
+  p.groups_per_xcd = (num_seqs * num_kv_heads + kXcds - 1) / kXcds;
   p.causal = causal;
   p.scale_log2 = scale * kLog2e;
   return launch_prefill<false>(p, head_dim, num_seqs, (hipStream_t)stream);
@@ -456,6 +786,8 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;
   p.num_m_blocks = (max_q_len + kBlockM - 1) / kBlockM;
+  p.num_seqs = num_seqs;
+  p.groups_per_xcd = (num_seqs * num_kv_heads + kXcds - 1) / kXcds;
   p.causal = causal;
   p.scale_log2 = scale * kLog2e;
   return launch_prefill<true>(p, head_dim, num_seqs, (hipStream_t)stream);
