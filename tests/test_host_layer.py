@@ -44,3 +44,28 @@ def test_ops_refuse_cpu_tensors():
     with pytest.raises(ValueError, match="GPU only"):
         ops.kv_write(q.view(2, 1, 4, 128)[:, :, :2], q.view(2, 1, 4, 128)[:, :, :2], kc, kc,
                      torch.zeros(2, 1, dtype=torch.int64))
+
+
+def test_mrope_with_equal_axes_is_1d_rope():
+    """Mirror of the reference's tests/unit/test_mrope.py:21-40 on the package layers."""
+    from nano_inference_amd.layers import MRotaryEmbedding, RotaryEmbedding
+
+    torch.manual_seed(0)
+    q = torch.randn(2, 5, 4, 128)
+    k = torch.randn(2, 5, 2, 128)
+    pos = torch.arange(5).unsqueeze(0).expand(2, -1) + 7
+    a = RotaryEmbedding(128, 1e6)(q, k, pos)
+    b = MRotaryEmbedding(128, 1e6, (16, 24, 24))(q, k, pos.unsqueeze(0).expand(3, -1, -1))
+    torch.testing.assert_close(a[0], b[0], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(a[1], b[1], atol=1e-5, rtol=1e-5)
+
+
+def test_rmsnorm_formula():
+    """RMSNorm = x / sqrt(mean(x^2) + eps) * w, fp32 inside (reference norm.py:35-47)."""
+    from nano_inference_amd.layers import RMSNorm
+
+    x = torch.randn(3, 7, 16, dtype=torch.float64)
+    n = RMSNorm(16, eps=1e-6).double()
+    n.weight.data = torch.linspace(0.5, 1.5, 16, dtype=torch.float64)
+    exp = x / torch.sqrt((x ** 2).mean(-1, keepdim=True) + 1e-6) * n.weight
+    torch.testing.assert_close(n(x), exp.to(x.dtype), atol=1e-6, rtol=1e-6)
