@@ -384,14 +384,20 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
 // ---------------------------------------------------------------------------------
 
 constexpr int kTileRowBytes = 256;                 // 128 bf16
+constexpr uint32_t kBf16OnePair = 0x3F803F80u;     // bf16 (1.0, 1.0)
 constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
 
 NIA_DEVICE int tile_swz(int r) { return ((r & 3) << 2) | ((r & 15) >> 2); }
 
-NIA_DEVICE void lds_dma16(const void* g, uint8_t* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                   (__attribute__((address_space(3))) void*)lds_wave_base, 16,
-                                   0, 0);
+// Buffer-resource word 3 for raw byte-addressed loads on gfx9-family parts
+// (DATA_FORMAT = 32-bit, all other fields zero).
+constexpr int kBufferWord3 = 0x00020000;
+
+// 16-byte DMA global -> LDS: lane i's 16 bytes at rsrc + voffset land at
+// lds_wave_base + 16 i.
+NIA_DEVICE void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voffset, 0, 0, 0);
 }
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -469,54 +475,72 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
   const int ld_pc = lane & 15;
   const int32_t* bt = PAGED ? p.block_tables + (int64_t)seq * p.bt_stride : nullptr;
   const int bs_mask = (1 << p.bs_log2) - 1;
-  // First key row of this wave's 16-row group in tile n0, clamped into the context.
-  auto group_key = [&](int n0) { return min(n0 + 16 * wave, klen - 1); };
+  // KV block holding this wave's 16-row group of tile n0 (first row clamped into the
+  // context); -1 for an invalid id.
   auto block_of = [&](int n0) __attribute__((always_inline)) -> int {
     if constexpr (PAGED) {
-      const int b = bt[uniform(group_key(n0) >> p.bs_log2)];
+      const int b = bt[uniform(min(n0 + 16 * wave, klen - 1) >> p.bs_log2)];
       return (b < 0 || (int64_t)b >= p.num_blocks) ? -1 : b;
     } else {
       return 0;
     }
   };
-  // Lane constants of the DMA: row rr[i] of the wave's 16-row group and the
-  // element offset of the swizzled 16-byte chunk it fetches.
-  int rr[4], cc[4];
+  // Lane constants of the DMA: lane (sub, pc) = (lane / 16, lane % 16) of instruction i
+  // fills row 4 i + sub of the wave's 16-row group at chunk position pc, which holds
+  // chunk pc ^ f(row).  For groups inside the context the lane's byte offset from the
+  // group's first row is loop-invariant (row strides stay below 2^26 elements, checked
+  // on the host, so it fits 32 bits).
+  const int64_t k_row = PAGED ? D : p.k_tok;
+  const int64_t v_row = PAGED ? D : p.v_tok;
+  uint32_t k_lane[4], v_lane[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    rr[i] = 4 * i + ld_sub;
-    cc[i] = 8 * (ld_pc ^ tile_swz(rr[i]));
+    const int r = 4 * i + ld_sub;
+    const int c = 8 * (ld_pc ^ tile_swz(r));
+    k_lane[i] = (uint32_t)(r * k_row + c) * 2u;
+    v_lane[i] = (uint32_t)(r * v_row + c) * 2u;
   }
-  auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
-    uint8_t* kdst = lds[stage][0] + wave * 16 * kTileRowBytes;
-    uint8_t* vdst = lds[stage][1] + wave * 16 * kTileRowBytes;
-    const int g0 = n0 + 16 * wave;        // first key of the group (uniform)
-    const int gk = min(g0, klen - 1);     // clamped into the context
-    const bool full = g0 + 15 < klen;
-    const bf16_t* kb;
-    const bf16_t* vb;
-    int64_t ks_row, vs_row;               // element stride between key rows
+  // First element of key row `row` of this KV head (contiguous) or of the row's slot in
+  // block `blk` (paged).  An invalid block id reads block 0 of the KV head: finite data,
+  // and the rows it feeds are masked.
+  auto row_base = [&](const bf16_t* base, int64_t tok, int64_t head, int row,
+                      int blk) __attribute__((always_inline)) -> const bf16_t* {
     if constexpr (PAGED) {
-      // An invalid block id reads block 0 of the KV head: finite data, and the
-      // rows it feeds are masked.
-      const int64_t base_row =
-          ((((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << p.bs_log2) + (gk & bs_mask));
-      kb = p.k + base_row * D;
-      vb = p.v + base_row * D;
-      ks_row = vs_row = D;
+      const int64_t r =
+          ((((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << p.bs_log2) + (row & bs_mask));
+      return base + r * D;
     } else {
-      kb = p.k + (kstart + gk) * p.k_tok + (int64_t)hk * p.k_head;
-      vb = p.v + (kstart + gk) * p.v_tok + (int64_t)hk * p.v_head;
-      ks_row = p.k_tok;
-      vs_row = p.v_tok;
+      return base + (kstart + row) * tok + (int64_t)hk * head;
     }
+  };
+  // DMA this wave's 16 rows of tile n0 (K or V) into `tile` with buffer loads whose
+  // resource spans exactly the 16 rows (a read past it would return zeros, never
+  // fault).  Rows past the context repeat the last key (masked later).
+  auto issue_rows = [&](const bf16_t* base, int64_t tok, int64_t head, int64_t row_stride,
+                        const uint32_t* lane_off, uint8_t* tile, int n0,
+                        int blk) __attribute__((always_inline)) {
+    uint8_t* dst = tile + wave * 16 * kTileRowBytes;
+    const int g0 = n0 + 16 * wave;
+    const int gk = min(g0, klen - 1);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)row_base(base, tok, head, gk, blk), 0, (int)((15 * row_stride + D) * 2),
+        kBufferWord3);
+    if (g0 + 15 < klen) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // Rows past the context repeat the last key (masked later).
-      const int dr = full ? rr[i] : min(g0 + rr[i], klen - 1) - gk;
-      lds_dma16(kb + dr * ks_row + cc[i], kdst + i * 1024);
-      lds_dma16(vb + dr * vs_row + cc[i], vdst + i * 1024);
+      for (int i = 0; i < 4; ++i) lds_dma16(rsrc, lane_off[i], dst + i * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + ld_sub;
+        const int dr = min(g0 + r, klen - 1) - gk;
+        lds_dma16(rsrc, (uint32_t)(dr * row_stride + 8 * (ld_pc ^ tile_swz(r))) * 2u,
+                  dst + i * 1024);
+      }
     }
+  };
+  auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
+    issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, lds[stage][0], n0, blk);
+    issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, lds[stage][1], n0, blk);
   };
 
   // ---- per-lane LDS read offsets ---------------------------------------------------------
@@ -594,8 +618,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
         for (int j = 0; j < 4; ++j) {
           const float p0 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub));
           const float p1 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub));
-          l_run += p0 + p1;
           w[j] = pack_bf16x2(p0, p1);
+          // Row sum of the bf16 probabilities the PV product uses (one dot2 per pair).
+          l_run = dot2_bf16(w[j], kBf16OnePair, l_run);
         }
         pb[2 * c + hh] = make_uint4(w[0], w[1], w[2], w[3]);
       }
@@ -653,6 +678,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
   }
 }
 
+constexpr int64_t kMaxRowStride = (int64_t)1 << 26;  // elements
+
 template <bool PAGED>
 int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream_t s) {
   const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd * p.group * p.num_m_blocks;
@@ -669,7 +696,9 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
       hipLaunchKernelGGL((prefill_kernel<96, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
       break;
     case 128:
-      if (!PAGED || p.bs_log2 >= 4)
+      // The DMA kernel needs 16-row groups inside one KV block and 32-bit lane offsets.
+      if (PAGED ? p.bs_log2 >= 4 : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
+                                    p.v_tok < kMaxRowStride))
         hipLaunchKernelGGL((prefill_d128_kernel<PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
       else
         hipLaunchKernelGGL((prefill_kernel<128, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
