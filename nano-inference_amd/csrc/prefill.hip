@@ -570,17 +570,27 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
     const uint8_t* vt = lds[stage][1];
     f32x16_t sacc[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[c][r] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < DK; ++kk) {
+    for (int kk = 0; kk < DK; ++kk) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
         const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kTileRowBytes + k_off[kk]);
         sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]), sacc[c], 0,
             0, 0);
       }
     }
+    // Issue order: K operand reads run six MFMAs ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
     if (n0 + kBlockN > wave_kmin) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
@@ -637,6 +647,14 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
             0, 0);
       }
     }
+    // Issue order: transposed V reads run four MFMAs ahead of the PV products.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
 
   // ---- main loop: tile n0 in lds[stage] while tile n0 + 64 streams into the other --------
