@@ -37,6 +37,7 @@ namespace {
 
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
+constexpr int kCombineThreads = 256;  // four (sequence, head) pairs per workgroup
 constexpr float kLazyRescale = 8.0f;
 
 struct DecodeParams {
@@ -336,35 +337,6 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_partial_kernel(De
   merge_waves_and_store<T, D, G>(p, o, m, l, row, col, wave, b, hk, part, nparts);
 }
 
-// Merge the partition partials of one (sequence, head); one thread per dim.
-// Sequences with at most one partition were finished by the partial kernel.
-template <typename T, int D, int BS, int PART_BLOCKS>
-__global__ __launch_bounds__(D) void paged_decode_combine_kernel(DecodeParams p) {
-  using E = Elem<T>;
-  constexpr int PART_TOKENS = PART_BLOCKS * BS;
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int d = threadIdx.x;
-  int64_t ctx64 = p.context_lens[b];
-  const int64_t cap = (int64_t)p.max_blocks * BS;
-  if (ctx64 > cap) ctx64 = cap;
-  const int ctx = ctx64 > 0 ? (int)ctx64 : 0;
-  const int nparts = (ctx + PART_TOKENS - 1) / PART_TOKENS;
-  if (nparts <= 1) return;  // finished (or zero-filled) by the partial kernel
-  T* out = reinterpret_cast<T*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h;
-  const int64_t slot0 = ((int64_t)b * p.num_heads + h) * p.max_parts;
-  float mt = -INFINITY;
-  for (int i = 0; i < nparts; ++i) mt = fmaxf(mt, p.ws_ml[(slot0 + i) * 2]);
-  float lt = 0.f, ot = 0.f;
-  for (int i = 0; i < nparts; ++i) {
-    const float mi = p.ws_ml[(slot0 + i) * 2];
-    const float wt = (mi == -INFINITY) ? 0.f : fast_exp2(mi - mt);
-    lt = fmaf(p.ws_ml[(slot0 + i) * 2 + 1], wt, lt);
-    ot = fmaf(p.ws_o[(slot0 + i) * D + d], wt, ot);
-  }
-  out[d] = E::from_f32(lt > 0.f ? ot / lt : 0.f);
-}
-
 // Wave-wide max (every lane receives the maximum over all 64 lanes).
 NIA_DEVICE float wave_max(float x) {
 #pragma unroll
@@ -376,6 +348,68 @@ NIA_DEVICE float wave_sum(float x) {
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
   return x;
+}
+
+// Merge the partition partials of (sequence, head) pairs: one wave per pair, each
+// lane owning D / 64 output dims.  Lane i first holds partition i's (m, l) (64 at a
+// time), so the global max and the weights exp2(m_i - M) take one load and two wave
+// reductions; the partial outputs are then accumulated eight partitions per round of
+// independent loads.  Pairs whose sequence has at most one partition were finished
+// by the partial kernel.
+template <typename T, int D, int BS, int PART_BLOCKS>
+__global__ __launch_bounds__(kCombineThreads) void paged_decode_combine_kernel(DecodeParams p,
+                                                                               int batch) {
+  using E = Elem<T>;
+  constexpr int PART_TOKENS = PART_BLOCKS * BS;
+  constexpr int DL = D / kWave;  // dims per lane
+  static_assert(DL == 2, "one float2 of output per lane");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int pair = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6);
+  if (pair >= batch * p.num_heads) return;
+  const int b = pair / p.num_heads;
+  const int h = pair - b * p.num_heads;
+  int64_t ctx64 = p.context_lens[b];
+  const int64_t cap = (int64_t)p.max_blocks * BS;
+  if (ctx64 > cap) ctx64 = cap;
+  const int ctx = ctx64 > 0 ? (int)ctx64 : 0;
+  const int nparts = (ctx + PART_TOKENS - 1) / PART_TOKENS;
+  if (nparts <= 1) return;
+  const int64_t slot0 = ((int64_t)b * p.num_heads + h) * p.max_parts;
+  const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + slot0;
+  float mt = -INFINITY;
+  for (int c0 = 0; c0 < nparts; c0 += kWave)
+    if (c0 + lane < nparts) mt = fmaxf(mt, ml[c0 + lane].x);
+  mt = wave_max(mt);
+  float lt = 0.f;
+  float2 acc = make_float2(0.f, 0.f);
+  const float* po = p.ws_o + slot0 * D + DL * lane;
+  for (int c0 = 0; c0 < nparts; c0 += kWave) {
+    float w = 0.f;
+    if (c0 + lane < nparts) {
+      const float2 v = ml[c0 + lane];
+      w = v.x == -INFINITY ? 0.f : fast_exp2(v.x - mt);
+      lt = fmaf(v.y, w, lt);
+    }
+    const int cnt = min(kWave, nparts - c0);
+    for (int j0 = 0; j0 < cnt; j0 += 8) {
+      float2 o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        o[j] = j0 + j < cnt ? *reinterpret_cast<const float2*>(po + (int64_t)(c0 + j0 + j) * D)
+                            : make_float2(0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float wj = __shfl(w, j0 + j, kWave);
+        acc.x = fmaf(o[j].x, wj, acc.x);
+        acc.y = fmaf(o[j].y, wj, acc.y);
+      }
+    }
+  }
+  lt = wave_sum(lt);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  T* out = reinterpret_cast<T*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h + DL * lane;
+  out[0] = E::from_f32(acc.x * inv);
+  out[1] = E::from_f32(acc.y * inv);
 }
 
 // bf16 decode, head_dim 128, block size 16 (the serving layout).
@@ -794,6 +828,15 @@ int persistent_grid(int device, int upper) {
 }
 
 template <typename T, int D, int BS>
+void launch_combine(const DecodeParams& p, int batch, hipStream_t s) {
+  constexpr int kPairsPerGroup = kCombineThreads / kWave;
+  const int pairs = batch * p.num_heads;
+  hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, kPartBlocks>),
+                     dim3((pairs + kPairsPerGroup - 1) / kPairsPerGroup), dim3(kCombineThreads), 0,
+                     s, p, batch);
+}
+
+template <typename T, int D, int BS>
 int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStream_t s) {
   constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
   if (kBf16 && batch <= kPersistentMaxBatch) {
@@ -821,9 +864,7 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
       default:
         return NIA_ERR_UNSUPPORTED;
     }
-    if (p.max_parts > 1)
-      hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, kPartBlocks>),
-                         dim3(p.num_heads, batch), dim3(D), 0, s, p);
+    if (p.max_parts > 1) launch_combine<T, D, BS>(p, batch, s);
     return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
   }
   const dim3 grid(p.max_parts, p.num_kv_heads, batch);
@@ -849,9 +890,7 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
     default:
       return NIA_ERR_UNSUPPORTED;
   }
-  if (p.max_parts > 1)
-    hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, kPartBlocks>),
-                       dim3(p.num_heads, batch), dim3(D), 0, s, p);
+  if (p.max_parts > 1) launch_combine<T, D, BS>(p, batch, s);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
