@@ -39,6 +39,9 @@ constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kCombineThreads = 256;  // four (sequence, head) pairs per workgroup
 constexpr float kLazyRescale = 8.0f;
+// Largest query-group size whose block loop keeps the next pair's K in flight
+// during P V (32 more VGPRs than the plain loop).
+constexpr int kRollingMaxG = 4;
 
 struct DecodeParams {
   void* out;
@@ -439,33 +442,47 @@ struct DecodeState {
   float m[G];
 };
 
-// Issue the 8 wave-wide loads of one block-head (4 K in the K layout, 4 V in the
-// V layout); an index past the partition or an invalid block id gives zeros.
-NIA_DEVICE bool decode_load_block(const DecodeParams& p, const bf16_t* kcache,
-                                  const bf16_t* vcache, int my_bt, int jx, int blk_begin,
-                                  int blk_end, int hk, int lane, uint4 (&kr)[4],
-                                  uint4 (&vr)[4]) {
+// Physical block of partition-relative block jx (its table entry sits in lane
+// jx - blk_begin of my_bt), or -1 past the partition or for an invalid id.
+NIA_DEVICE int decode_block_id(const DecodeParams& p, int my_bt, int jx, int blk_begin,
+                               int blk_end) {
+  const int blk = jx < blk_end ? __builtin_amdgcn_readlane(my_bt, jx - blk_begin) : -1;
+  return (blk >= 0 && (int64_t)blk < p.num_blocks) ? blk : -1;
+}
+
+// The 4 wave-wide loads of one block-head's K in the K layout (lane: token
+// lane / 8 and + 8, 16-dim chunk lane % 8); zeros for blk < 0.
+NIA_DEVICE void decode_load_k(const DecodeParams& p, const bf16_t* kcache, int blk, int hk,
+                              int lane, uint4 (&kr)[4]) {
   constexpr int BS = 16, D = 128;
   const int ktok = lane >> 3, kc = lane & 7;
-  const int blk = jx < blk_end ? __builtin_amdgcn_readlane(my_bt, jx - blk_begin) : -1;
-  const bool ok = blk >= 0 && (int64_t)blk < p.num_blocks;
-  if (ok) {
-    const int64_t base = ((int64_t)blk * p.num_kv_heads + hk) * (BS * D);
-    const uint4* kp = reinterpret_cast<const uint4*>(kcache + base);
-    const uint4* vp = reinterpret_cast<const uint4*>(vcache + base);
+  if (blk >= 0) {
+    const uint4* kp =
+        reinterpret_cast<const uint4*>(kcache + ((int64_t)blk * p.num_kv_heads + hk) * (BS * D));
     kr[0] = kp[ktok * 16 + 2 * kc];
     kr[1] = kp[ktok * 16 + 2 * kc + 1];
     kr[2] = kp[(ktok + 8) * 16 + 2 * kc];
     kr[3] = kp[(ktok + 8) * 16 + 2 * kc + 1];
+  } else {
+    kr[0] = kr[1] = kr[2] = kr[3] = make_uint4(0, 0, 0, 0);
+  }
+}
+
+// The 4 wave-wide loads of one block-head's V in the V layout (lane: token
+// 4 i + lane / 16, 8-dim chunk lane % 16); zeros for blk < 0.
+NIA_DEVICE void decode_load_v(const DecodeParams& p, const bf16_t* vcache, int blk, int hk,
+                              int lane, uint4 (&vr)[4]) {
+  constexpr int BS = 16, D = 128;
+  if (blk >= 0) {
+    const uint4* vp =
+        reinterpret_cast<const uint4*>(vcache + ((int64_t)blk * p.num_kv_heads + hk) * (BS * D));
     vr[0] = vp[lane];
     vr[1] = vp[64 + lane];
     vr[2] = vp[128 + lane];
     vr[3] = vp[192 + lane];
   } else {
-    kr[0] = kr[1] = kr[2] = kr[3] = make_uint4(0, 0, 0, 0);
     vr[0] = vr[1] = vr[2] = vr[3] = make_uint4(0, 0, 0, 0);
   }
-  return ok;
 }
 
 // Zero the V rows of one 16-token block (V layout) that lie past the context
@@ -482,16 +499,14 @@ NIA_DEVICE void zero_invalid_v(uint4 (&v)[4], bool ok, int tok0, int ctx, int vr
   }
 }
 
+// Scores of a block pair (K layout), pre-scaled to log2 units; -inf past the
+// context or in an invalid block.
 template <int G>
-NIA_DEVICE void decode_compute_pair(const DecodeParams& p, DecodeState<G>& st,
-                                    const uint4 (&kA)[4], const uint4 (&kB)[4],
-                                    uint4 (&vA)[4], uint4 (&vB)[4], bool okA, bool okB,
-                                    int jb, int ctx, int lane) {
+NIA_DEVICE void decode_qk_pair(const DecodeParams& p, const DecodeState<G>& st,
+                               const uint4 (&kA)[4], const uint4 (&kB)[4], bool okA, bool okB,
+                               int jb, int ctx, int lane, float (&xs)[2][2][G]) {
   constexpr int BS = 16;
   const int ktok = lane >> 3;
-  const int vrow = lane >> 4;
-  // ---- scores (K layout) ----------------------------------------------------------------
-  float xs[2][2][G];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
@@ -514,6 +529,15 @@ NIA_DEVICE void decode_compute_pair(const DecodeParams& p, DecodeState<G>& st,
       }
     }
   }
+}
+
+// Online-softmax update and O += P V for a block pair (V layout).
+template <int G>
+NIA_DEVICE void decode_pv_pair(const DecodeParams& p, DecodeState<G>& st,
+                               const float (&xs)[2][2][G], uint4 (&vA)[4], uint4 (&vB)[4],
+                               bool okA, bool okB, int jb, int ctx, int lane) {
+  constexpr int BS = 16;
+  const int vrow = lane >> 4;
   // ---- lazy wave-uniform running max -------------------------------------------------------
   float bm[G];
   bool need = false;
@@ -628,13 +652,57 @@ NIA_DEVICE void decode_bf16_item(const DecodeParams& p, int b, int hk, int part,
 
   {
     constexpr int kStep = 2 * kDecodeWaves;
-    for (int jb = blk_begin + 2 * wave; jb < blk_end; jb += kStep) {
-      uint4 kA[4], vA[4], kB[4], vB[4];
-      const bool okA =
-          decode_load_block(p, kcache, vcache, my_bt, jb, blk_begin, blk_end, hk, lane, kA, vA);
-      const bool okB = decode_load_block(p, kcache, vcache, my_bt, jb + 1, blk_begin, blk_end,
-                                         hk, lane, kB, vB);
-      decode_compute_pair<G>(p, st, kA, kB, vA, vB, okA, okB, jb, ctx, lane);
+    if constexpr (G <= kRollingMaxG) {
+      // Rolling pipeline: the next pair's K loads go out as soon as this pair's
+      // scores are taken, its V loads as soon as this pair's P V is issued, so a wave
+      // keeps loads in flight while it computes.
+      int jb = blk_begin + 2 * wave;
+      if (jb < blk_end) {
+        uint4 kA[4], vA[4], kB[4], vB[4];
+        int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
+        int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
+        decode_load_k(p, kcache, bA, hk, lane, kA);
+        decode_load_v(p, vcache, bA, hk, lane, vA);
+        decode_load_k(p, kcache, bB, hk, lane, kB);
+        decode_load_v(p, vcache, bB, hk, lane, vB);
+        for (;;) {
+          float xs[2][2][G];
+          decode_qk_pair<G>(p, st, kA, kB, bA >= 0, bB >= 0, jb, ctx, lane, xs);
+          const int jn = jb + kStep;
+          const bool more = jn < blk_end;
+          int nA = -1, nB = -1;
+          // The next pair's loads reuse this pair's registers: keep them behind the
+          // instructions that read those registers.
+          __builtin_amdgcn_sched_barrier(0);
+          if (more) {
+            nA = decode_block_id(p, my_bt, jn, blk_begin, blk_end);
+            nB = decode_block_id(p, my_bt, jn + 1, blk_begin, blk_end);
+            decode_load_k(p, kcache, nA, hk, lane, kA);
+            decode_load_k(p, kcache, nB, hk, lane, kB);
+          }
+          decode_pv_pair<G>(p, st, xs, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
+          if (!more) break;
+          __builtin_amdgcn_sched_barrier(0);
+          decode_load_v(p, vcache, nA, hk, lane, vA);
+          decode_load_v(p, vcache, nB, hk, lane, vB);
+          bA = nA;
+          bB = nB;
+          jb = jn;
+        }
+      }
+    } else {
+      for (int jb = blk_begin + 2 * wave; jb < blk_end; jb += kStep) {
+        uint4 kA[4], vA[4], kB[4], vB[4];
+        const int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
+        const int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
+        decode_load_k(p, kcache, bA, hk, lane, kA);
+        decode_load_v(p, vcache, bA, hk, lane, vA);
+        decode_load_k(p, kcache, bB, hk, lane, kB);
+        decode_load_v(p, vcache, bB, hk, lane, vB);
+        float xs[2][2][G];
+        decode_qk_pair<G>(p, st, kA, kB, bA >= 0, bB >= 0, jb, ctx, lane, xs);
+        decode_pv_pair<G>(p, st, xs, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
+      }
     }
   }
 
@@ -698,7 +766,7 @@ constexpr int kPersistentMaxBatch = 4096;
 // before the first call, and the last workgroup to leave returns them to zero.
 template <int G, int PART_BLOCKS>
 __global__ __launch_bounds__(kDecodeThreads)
-__attribute__((amdgpu_waves_per_eu(G <= 4 ? 3 : 2))) void paged_decode_bf16_persistent_kernel(
+__attribute__((amdgpu_waves_per_eu(G <= kRollingMaxG ? 2 : 2))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
   __shared__ int s_prefix[kPersistentMaxBatch + 1];
