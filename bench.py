@@ -186,6 +186,22 @@ def bench_decode_vl(torch, ops, workloads):
                 bytes=c.decode_bytes())
 
 
+def bench_e2e(torch):
+    """Whole-model generation on the Qwen3-0.6B architecture (random-initialised bf16):
+    64 prompts of U[128, 2048] random ids, 256 greedy tokens each, decode step in a
+    HIP graph.  Throughput = (prompt + generated tokens) / elapsed."""
+    from nano_inference_amd import e2e
+
+    gen = e2e.build(use_graph=True)
+    gen.run([pr[:64] for pr in gen.prompts[:4]])  # warm-up
+    st = gen.run(gen.prompts)
+    return dict(tokens_per_s=round(st.tokens_per_s, 1),
+                decode_tokens_per_s=round(st.decode_tokens_per_s, 1),
+                prompt_tokens=st.prompt_tokens, generated_tokens=st.generated_tokens,
+                prefill_s=round(st.prefill_s, 4), decode_s=round(st.decode_s, 4),
+                total_s=round(st.total_s, 4))
+
+
 def cpu_baseline(torch, workloads, budget_s: float = 20.0):
     """The reference's decode attention (op-for-op CPU restatement), fp32, on a sample.
 
@@ -263,6 +279,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--profile-decode", type=int, default=0)
     ap.add_argument("--profile-prefill", type=int, default=0)
+    ap.add_argument("--no-e2e", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -292,6 +309,8 @@ def main() -> int:
     pf = extra["prefill_qwen3_8b"]
     extra["kv_write_qwen3_8b"] = dict(us=round(wr_ms * 1e3, 2),
                                       gbps=round(c.write_bytes() / (wr_ms * 1e-3) / 1e9, 1))
+    if not args.no_e2e:
+        extra["e2e_qwen3_0p6b"] = bench_e2e(torch)
     line = {
         "metric": "decode attn HBM GB/s (% of peak) + prefill attn TFLOP/s (% bf16 MFMA peak)",
         "value": round(value, 1),

@@ -9,7 +9,9 @@ with PyTorch-side layers that keep the reference engine's attention interface:
                    ``scaled_dot_product_attention`` as drop-ins for
                    src/nano_inference/layers/attention.py;
 * ``vision``     - ``VisionAttention`` (Qwen2.5-VL ViT) and its chunk producers;
-* ``context``    - ``AttentionMetadata``, field-for-field the reference's.
+* ``context``    - ``AttentionMetadata``, field-for-field the reference's;
+* ``e2e``        - a Qwen3-architecture decoder over these layers with a paged KV
+                   pool and a batched greedy generator (whole-model throughput).
 """
 from . import _lib, ops  # noqa: F401
 from .attention import (  # noqa: F401
