@@ -44,18 +44,33 @@ def _events(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_calls(torch, fn, iters: int, warmup: int = 3) -> float:
-    """Average milliseconds per call of fn (events on the current stream)."""
-    for _ in range(warmup):
-        fn(0)
-    torch.cuda.synchronize()
-    a, b = _events(torch)
-    a.record()
-    for i in range(iters):
-        fn(i)
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / iters
+def warm_up(torch, fn, seconds: float = 0.1) -> None:
+    """Run fn until `seconds` of wall time have passed.  The GPU raises its clocks over
+    the first few milliseconds of sustained work (and lowers them when idle), so every
+    measured leg first runs its own work for a while."""
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
+def time_calls(torch, fn, iters: int, rounds: int = 5) -> float:
+    """Milliseconds per call of fn: after a warm-up, `rounds` batches of `iters`
+    back-to-back calls are timed with events; the median batch mean is returned."""
+    warm_up(torch, fn)
+    means = []
+    for _ in range(rounds):
+        a, b = _events(torch)
+        a.record()
+        for i in range(iters):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        means.append(a.elapsed_time(b) / iters)
+    return sorted(means)[len(means) // 2]
 
 
 def per_call_ms(torch, fn, iters: int) -> float:
@@ -69,6 +84,28 @@ def per_call_ms(torch, fn, iters: int) -> float:
         pairs.append((a, b))
     torch.cuda.synchronize()
     return sum(a.elapsed_time(b) for a, b in pairs) / iters
+
+
+def graph_call_ms(torch, fn, calls: int = 50, rounds: int = 5) -> float:
+    """Device time per call of a short kernel: `calls` calls captured in one HIP graph,
+    replayed `rounds` times after a warm-up; median replay time / calls.  (Timed one
+    by one, a kernel of a few microseconds measures the host's launch rate instead.)"""
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(calls):
+            fn(i)
+    warm_up(torch, lambda _: g.replay(), 0.05)
+    times = []
+    for _ in range(rounds):
+        a, b = _events(torch)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / calls)
+    return sorted(times)[len(times) // 2]
 
 
 def read_traffic(workload: str):
@@ -107,6 +144,7 @@ def bench_decode(torch, ops, workloads, steps: int, warmup: int):
         write(i)
         decode(i)
 
+    warm_up(torch, step)
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -119,7 +157,7 @@ def bench_decode(torch, ops, workloads, steps: int, warmup: int):
     ms_step = a.elapsed_time(e) / steps
     iters = max(steps, 20)
     dec_ms = per_call_ms(torch, decode, iters)
-    wr_ms = per_call_ms(torch, write, iters)
+    wr_ms = graph_call_ms(torch, lambda _: write(0))
     return c, ms_step, dec_ms, wr_ms
 
 
@@ -178,8 +216,7 @@ def bench_decode_vl(torch, ops, workloads):
         ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens,
                          out=out)
 
-    for i in range(5):
-        decode(i)
+    warm_up(torch, decode)
     ms = per_call_ms(torch, decode, 40)
     gbps = c.decode_bytes() / (ms * 1e-3) / 1e9
     return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
