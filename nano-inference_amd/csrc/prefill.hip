@@ -363,10 +363,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
 }
 
 // ---------------------------------------------------------------------------------
-// head_dim 128 kernel: K/V tiles stream global -> LDS by direct DMA
-// (global_load_lds_dwordx4), double-buffered, and the V^T MFMA operand is read
-// with ds_read_b64_tr_b16 from a row-major V tile, so no VGPR staging, no
+// DMA kernel (head_dim 64, 80, 96, 128): K/V tiles stream global -> LDS by direct DMA
+// (buffer loads with an LDS destination), double-buffered, and the V^T MFMA operand
+// is read with ds_read_b64_tr_b16 from a row-major V tile, so no VGPR staging, no
 // ds_write and no transpose work remains on the VALU.
+//
+// Rows are laid out for head_dim 128 whatever D is: a smaller D fetches only its
+// D / 8 chunks of each row, the QK product contracts over its D / 16 steps, and the
+// last PV tile of 32 dims (D = 80 or 96) runs over unfetched LDS columns whose
+// output rows are never stored.
 //
 // LDS tile layout (K and V alike): 64 rows x 256 B, 16-byte chunk c of row r
 // stored at chunk position c ^ f(r), f(r) = 4 (r & 3) + ((r & 15) >> 2).  A row
@@ -410,11 +415,12 @@ NIA_DEVICE s16x4_t lds_read_tr16(const uint8_t* addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)addr);
 }
 
-template <bool PAGED>
-__global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(PrefillParams p) {
-  constexpr int D = 128;
-  constexpr int DK = D / 16;
-  constexpr int DT = D / 32;
+template <int D, bool PAGED>
+__global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(PrefillParams p) {
+  static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
+  constexpr int DK = D / 16;              // QK steps of 16 dims
+  constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
+  constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2][kTileBytes];  // [stage][K, V]
 
   int seq, h, mb;
@@ -493,12 +499,14 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
   const int64_t k_row = PAGED ? D : p.k_tok;
   const int64_t v_row = PAGED ? D : p.v_tok;
   uint32_t k_lane[4], v_lane[4];
+  bool chunk_ok[4];  // the lane's chunk lies inside the D-wide row (always, for D = 128)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * i + ld_sub;
-    const int c = 8 * (ld_pc ^ tile_swz(r));
-    k_lane[i] = (uint32_t)(r * k_row + c) * 2u;
-    v_lane[i] = (uint32_t)(r * v_row + c) * 2u;
+    const int c = ld_pc ^ tile_swz(r);
+    chunk_ok[i] = c < kChunks;
+    k_lane[i] = (uint32_t)(r * k_row + 8 * c) * 2u;
+    v_lane[i] = (uint32_t)(r * v_row + 8 * c) * 2u;
   }
   // First element of key row `row` of this KV head (contiguous) or of the row's slot in
   // block `blk` (paged).  An invalid block id reads block 0 of the KV head: finite data,
@@ -527,14 +535,16 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
         kBufferWord3);
     if (g0 + 15 < klen) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lds_dma16(rsrc, lane_off[i], dst + i * 1024);
+      for (int i = 0; i < 4; ++i)
+        if (kChunks == 16 || chunk_ok[i]) lds_dma16(rsrc, lane_off[i], dst + i * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 4 * i + ld_sub;
         const int dr = min(g0 + r, klen - 1) - gk;
-        lds_dma16(rsrc, (uint32_t)(dr * row_stride + 8 * (ld_pc ^ tile_swz(r))) * 2u,
-                  dst + i * 1024);
+        if (kChunks == 16 || chunk_ok[i])
+          lds_dma16(rsrc, (uint32_t)(dr * row_stride + 8 * (ld_pc ^ tile_swz(r))) * 2u,
+                    dst + i * 1024);
       }
     }
   };
@@ -689,9 +699,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_d128_kernel(Prefil
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = 32 * dt + 8 * g + 4 * half;
-      const uint2 val = make_uint2(pack_bf16x2(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv),
-                                   pack_bf16x2(oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv));
-      *reinterpret_cast<uint2*>(op + d) = val;
+      if (d < D) {  // the padded dims of the last tile are never stored
+        const uint2 val =
+            make_uint2(pack_bf16x2(oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv),
+                       pack_bf16x2(oacc[dt][4 * g + 2] * inv, oacc[dt][4 * g + 3] * inv));
+        *reinterpret_cast<uint2*>(op + d) = val;
+      }
     }
   }
 }
@@ -703,24 +716,24 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
   const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd * p.group * p.num_m_blocks;
   if (nwg >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
   const dim3 grid((unsigned)nwg);
+  // The DMA kernel needs 16-row groups inside one KV block and 32-bit lane offsets;
+  // the register-staged kernel serves the rest.
+  const bool dma_ok = PAGED ? p.bs_log2 >= 4
+                            : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
+                               p.v_tok < kMaxRowStride);
   switch (head_dim) {
-    case 64:
-      hipLaunchKernelGGL((prefill_kernel<64, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
-      break;
-    case 80:
-      hipLaunchKernelGGL((prefill_kernel<80, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
-      break;
-    case 96:
-      hipLaunchKernelGGL((prefill_kernel<96, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
-      break;
-    case 128:
-      // The DMA kernel needs 16-row groups inside one KV block and 32-bit lane offsets.
-      if (PAGED ? p.bs_log2 >= 4 : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
-                                    p.v_tok < kMaxRowStride))
-        hipLaunchKernelGGL((prefill_d128_kernel<PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
-      else
-        hipLaunchKernelGGL((prefill_kernel<128, PAGED>), grid, dim3(kPrefillThreads), 0, s, p);
-      break;
+#define NIA_PREFILL_CASE(DD)                                                                 \
+  case DD:                                                                                   \
+    if (dma_ok)                                                                              \
+      hipLaunchKernelGGL((prefill_dma_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), 0, s, p); \
+    else                                                                                     \
+      hipLaunchKernelGGL((prefill_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), 0, s, p); \
+    break;
+    NIA_PREFILL_CASE(64)
+    NIA_PREFILL_CASE(80)
+    NIA_PREFILL_CASE(96)
+    NIA_PREFILL_CASE(128)
+#undef NIA_PREFILL_CASE
     default:
       return NIA_ERR_UNSUPPORTED;
   }
