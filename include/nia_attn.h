@@ -160,6 +160,43 @@ int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_st
                           int64_t num_blocks, float scale, int32_t causal, int32_t dtype,
                           void* stream);
 
+/*
+ * Fused QK-RMSNorm + RoPE / mRoPE + KV-cache write, in place on q and k.
+ * Replaces the steps between the projections and attention in
+ * src/nano_inference/layers/attention.py:254-278: q_norm / k_norm
+ * (src/nano_inference/layers/norm.py:35-47), the rotary embedding
+ * (src/nano_inference/layers/rotary.py:8-33, :104-130; 3-axis mRoPE :184-210) and
+ * the cache write loop, with the same fp32 computation and the same rounding to
+ * the model dtype after every PyTorch op (only the order of the RMSNorm sum of
+ * squares differs, which can change the last bit of a value on a rounding boundary).
+ *   q [num_tokens, num_heads, 128], k and v [num_tokens, num_kv_heads, 128] with
+ *     element strides (tok, head); q and k are overwritten with their normalised,
+ *     rotated values.
+ *   q_norm_weight, k_norm_weight  [128] in the model dtype, or NULL for no QK norm
+ *     (both are applied when given; eps as the reference module's).
+ *   positions  [num_axes][num_tokens] int64 with axis stride pos_axis_stride:
+ *     num_axes 1 = RoPE position ids, 3 = mRoPE (temporal, height, width), whose
+ *     frequency i uses axis 0 for i < mrope_section0, axis 1 for
+ *     i < mrope_section0 + mrope_section1, else axis 2.
+ *   inv_freq  [64] fp32, the module's table (base^(-2i / 128)).
+ *   k_cache, v_cache  one layer [num_blocks, num_kv_heads, block_size, 128], or NULL
+ *     for no write; tokens whose slot_mapping entry is < 0 or >= num_blocks *
+ *     block_size are not written (as nia_kv_write).
+ * Supported: head_dim 128; dtype bf16 or f32.
+ */
+int32_t nia_qk_norm_rope_kv_write(void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                  void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                  const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                  const void* q_norm_weight, const void* k_norm_weight,
+                                  float eps, const int64_t* positions,
+                                  int64_t pos_axis_stride, int32_t num_axes,
+                                  const float* inv_freq, int32_t mrope_section0,
+                                  int32_t mrope_section1, void* k_cache, void* v_cache,
+                                  const int64_t* slot_mapping, int32_t num_tokens,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int64_t num_blocks, int32_t dtype,
+                                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

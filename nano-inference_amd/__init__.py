@@ -4,7 +4,8 @@ Hand-written HIP kernels behind a C ABI (libnia_attn.so, include/nia_attn.h),
 with PyTorch-side layers that keep the reference engine's attention interface:
 
 * ``ops``        - tensor-level wrappers of the C ABI (kv_write, paged_decode,
-                   prefill, varlen_attention, prefill_paged);
+                   prefill, varlen_attention, prefill_paged, and the fused
+                   qk_norm_rope_kv_write that feeds them);
 * ``attention``  - ``PagedCausalSelfAttention``, ``Qwen25VLDecoderAttention`` and
                    ``scaled_dot_product_attention`` as drop-ins for
                    src/nano_inference/layers/attention.py;

@@ -57,6 +57,11 @@ SIGNATURES = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p, _p, _p,
          _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _i32, _i32, _p],
     ),
+    "nia_qk_norm_rope_kv_write": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _p, _i64, _i32,
+         _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p],
+    ),
 }
 
 ABI_VERSION = 1

@@ -136,21 +136,43 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         self.k_norm = RMSNorm(hd) if use_qk_norm else None
         self.rotary = RotaryEmbedding(head_dim=hd, base=rope_base)
         self.layer_idx: Optional[int] = None
+        # QK-norm, RoPE and the cache write in one fused kernel (head_dim 128 on the
+        # GPU); False keeps the PyTorch ops.
+        self.fused_qk = True
 
     def _apply_rotary(self, q, k, position_ids, metadata=None) -> Tuple[torch.Tensor, torch.Tensor]:
         return self.rotary(q, k, position_ids)
 
-    def _qkv(self, x, position_ids, metadata):
+    def _rope_positions(self, position_ids, metadata):
+        """(positions, mrope_section) for the fused kernel: 1-D RoPE here."""
+        return position_ids, None
+
+    def _qkv(self, x, position_ids, metadata, k_cache=None, v_cache=None):
+        """Projected, normalised and rotated q, k and v; the last item tells whether
+        k/v were also written to (k_cache, v_cache) through the metadata's slots."""
         b, s, _ = x.shape
         q = self.q_proj(x).view(b, s, self.num_heads, self.head_dim)
         k = self.k_proj(x).view(b, s, self.num_kv_heads, self.head_dim)
         v = self.v_proj(x).view(b, s, self.num_kv_heads, self.head_dim)
+        if self.fused_qk and x.is_cuda and self.head_dim == 128 and \
+                x.dtype in (torch.bfloat16, torch.float32):
+            pos, section = self._rope_positions(position_ids, metadata)
+            write = k_cache is not None and metadata is not None and \
+                metadata.slot_mapping is not None
+            norm = self.q_norm is not None
+            ops.qk_norm_rope_kv_write(
+                q, k, v, self.q_norm.weight if norm else None,
+                self.k_norm.weight if norm else None, self.q_norm.eps if norm else 0.0,
+                pos, self.rotary.inv_freq, section,
+                k_cache if write else None, v_cache if write else None,
+                metadata.slot_mapping if write else None)
+            return q, k, v, write
         if self.q_norm is not None:
             q = self.q_norm(q)
         if self.k_norm is not None:
             k = self.k_norm(k)
         q, k = self._apply_rotary(q, k, position_ids, metadata)
-        return q, k, v
+        return q, k, v, False
 
     def _dense_causal(self, q, k, v, attention_mask):
         """No-cache path (metadata None): causal attention over the step's K/V."""
@@ -174,8 +196,8 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         metadata: Optional[AttentionMetadata] = None,
     ) -> torch.Tensor:
         b, s, _ = x.shape
-        q, k, v = self._qkv(x, position_ids, metadata)
         if metadata is None:
+            q, k, v, _ = self._qkv(x, position_ids, None)
             attn = self._dense_causal(q, k, v, attention_mask)
             return self.o_proj(attn.view(b, s, self.num_heads * self.head_dim))
         assert self.layer_idx is not None, "layer_idx must be set for PagedCausalSelfAttention"
@@ -184,9 +206,11 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         if metadata.k_cache is not None and metadata.v_cache is not None:
             k_cache = metadata.k_cache[self.layer_idx]
             v_cache = metadata.v_cache[self.layer_idx]
+        q, k, v, written = self._qkv(x, position_ids, metadata, k_cache, v_cache)
 
-        # 1. KV write (src/nano_inference/layers/attention.py:267-278).
-        if k_cache is not None and metadata.slot_mapping is not None:
+        # 1. KV write (src/nano_inference/layers/attention.py:267-278), unless the
+        # fused QK kernel already wrote the step's rows.
+        if not written and k_cache is not None and metadata.slot_mapping is not None:
             ops.kv_write(k, v, k_cache, v_cache, metadata.slot_mapping)
 
         if metadata.is_prefill:
@@ -223,9 +247,13 @@ class Qwen25VLDecoderAttention(PagedCausalSelfAttention):
         self.rotary = MRotaryEmbedding(head_dim=self.head_dim, base=self.rotary.base,
                                        mrope_section=mrope_section)
 
-    def _apply_rotary(self, q, k, position_ids, metadata=None):
+    def _mrope_ids(self, position_ids, metadata):
         if metadata is not None and metadata.mrope_position_ids is not None:
-            pos = metadata.mrope_position_ids
-        else:
-            pos = position_ids.unsqueeze(0).expand(3, -1, -1)
-        return self.rotary(q, k, pos)
+            return metadata.mrope_position_ids
+        return position_ids.unsqueeze(0).expand(3, -1, -1)
+
+    def _apply_rotary(self, q, k, position_ids, metadata=None):
+        return self.rotary(q, k, self._mrope_ids(position_ids, metadata))
+
+    def _rope_positions(self, position_ids, metadata):
+        return self._mrope_ids(position_ids, metadata), self.rotary._section_freqs

@@ -9,7 +9,7 @@ point of libnia_attn.so on the current HIP stream.  A nonzero status raises
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -376,3 +376,101 @@ def prefill_paged(
     )
     _lib.check("nia_prefill_paged", st)
     return out
+
+
+# ---------------------------------------------------------------------------------
+# Fused QK-RMSNorm + RoPE / mRoPE + KV write
+# ---------------------------------------------------------------------------------
+
+
+def qk_norm_rope_kv_write(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_norm_weight: Optional[torch.Tensor],
+    k_norm_weight: Optional[torch.Tensor],
+    eps: float,
+    positions: torch.Tensor,
+    inv_freq: torch.Tensor,
+    mrope_section: Optional[Tuple[int, int, int]] = None,
+    k_cache: Optional[torch.Tensor] = None,
+    v_cache: Optional[torch.Tensor] = None,
+    slot_mapping: Optional[torch.Tensor] = None,
+) -> None:
+    """QK-RMSNorm, RoPE (or mRoPE) in place on q and k, then the KV-cache write.
+
+    Same values as ``q_norm(q)``, ``k_norm(k)``, the rotary module and the write loop
+    of src/nano_inference/layers/attention.py:254-278 (every intermediate rounded to
+    the model dtype as the PyTorch ops round it).
+    q: (..., H, 128); k, v: (..., H_kv, 128) with the same leading dims (tokens);
+    positions: the leading dims' position ids, or (3, *leading) for mRoPE with
+    ``mrope_section``; inv_freq: (64,) (any float dtype); norm weights (128,) or None (no QK
+    norm; both or neither); caches one layer [num_blocks, H_kv, BS, 128] or None.
+    """
+    dev = _require_gpu(q, k, v, positions, inv_freq)
+    d = q.shape[-1]
+    if k.shape[-1] != d or v.shape != k.shape or q.shape[:-2] != k.shape[:-2]:
+        raise ValueError("q (..., H, D), k and v (..., H_kv, D) with the same leading dims")
+    if (q_norm_weight is None) != (k_norm_weight is None):
+        raise ValueError("q and k norm weights must both be given or both be None")
+    dt = _dtype_code(q)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k and v must share one dtype")
+    lead = q.shape[:-2]
+    n = math.prod(lead)
+    try:  # q and k are updated in place, so they must be viewable as (tokens, heads, D)
+        q2 = q.view(n, q.shape[-2], d)
+        k2 = k.view(n, k.shape[-2], d)
+    except RuntimeError as e:
+        raise ValueError(f"q and k must be viewable as (tokens, heads, D): {e}") from None
+    v2 = v.reshape(n, v.shape[-2], d)
+    for name, t in (("q", q2), ("k", k2), ("v", v2)):
+        _last_contig(name, t)
+    if mrope_section is None:
+        if positions.shape != lead:
+            raise ValueError(f"positions must have shape {tuple(lead)}")
+        num_axes, sec0, sec1 = 1, 0, 0
+    else:
+        if positions.shape != (3, *lead):
+            raise ValueError(f"mRoPE positions must have shape (3, {tuple(lead)})")
+        num_axes, sec0, sec1 = 3, int(mrope_section[0]), int(mrope_section[1])
+    pos = positions.reshape(num_axes, n).to(torch.int64).contiguous()
+    if not inv_freq.is_floating_point() or inv_freq.numel() != d // 2:
+        raise ValueError(f"inv_freq must be a ({d // 2},) floating-point table")
+    # A module cast to the model dtype holds a rounded table; the products
+    # position * inv_freq are still formed in fp32 from those rounded values.
+    inv = inv_freq.to(torch.float32).contiguous()
+    qw = kw = None
+    if q_norm_weight is not None:
+        if q_norm_weight.shape != (d,) or k_norm_weight.shape != (d,) or \
+                q_norm_weight.dtype != q.dtype or k_norm_weight.dtype != q.dtype:
+            raise ValueError(f"norm weights must be ({d},) in the model dtype")
+        qw, kw = q_norm_weight.contiguous(), k_norm_weight.contiguous()
+    kc_ptr = vc_ptr = sl_ptr = None
+    bs, nb = 1, 0
+    keep = []
+    if k_cache is not None:
+        if v_cache is None or slot_mapping is None:
+            raise ValueError("a cache write needs v_cache and slot_mapping")
+        if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or \
+                k_cache.shape[1] != k2.shape[1] or k_cache.shape[3] != d:
+            raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, D]")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("k_cache/v_cache layer slices must be contiguous")
+        if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+            raise ValueError("caches must share the model dtype")
+        if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
+            raise ValueError(f"slot_mapping must be int64 with {n} entries")
+        slots = slot_mapping.reshape(-1).contiguous()
+        keep.append(slots)
+        nb, bs = k_cache.shape[0], k_cache.shape[2]
+        kc_ptr, vc_ptr, sl_ptr = k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr()
+    lib = _lib.load()
+    st = lib.nia_qk_norm_rope_kv_write(
+        q2.data_ptr(), q2.stride(0), q2.stride(1), k2.data_ptr(), k2.stride(0), k2.stride(1),
+        v2.data_ptr(), v2.stride(0), v2.stride(1),
+        qw.data_ptr() if qw is not None else None, kw.data_ptr() if kw is not None else None,
+        float(eps), pos.data_ptr(), pos.stride(0), num_axes, inv.data_ptr(), sec0, sec1,
+        kc_ptr, vc_ptr, sl_ptr, n, q2.shape[1], k2.shape[1], d, bs, nb, dt, _stream(dev),
+    )
+    _lib.check("nia_qk_norm_rope_kv_write", st)

@@ -19,6 +19,9 @@ Modules
                        (src/nano_inference/engine/context_builder.py:83-193).
   vision_windows       restatement of the ViT window permutation and cu_seqlens
                        (src/nano_inference/layers/vision.py:365-412, :443-453).
+  qk_rope              op-for-op restatement of QK-RMSNorm and RoPE / mRoPE
+                       (layers/norm.py:35-47, layers/rotary.py:8-33, :105-130,
+                       :184-210), the steps in front of the KV write.
 
 Pinning (what checks each function; see tests/test_oracle_*.py)
   reference_attention.sdpa          torch.nn.functional.scaled_dot_product_attention
@@ -33,6 +36,11 @@ Pinning (what checks each function; see tests/test_oracle_*.py)
   textbook.*                        brute force on tiny inputs; closed forms; a planted
                                     mistake (wrong GQA map, dropped scale) must fail.
   metadata.*                        KATs of tests/unit/test_context_builder.py.
+  qk_rope.*                         KATs and properties of tests/unit/test_norm.py,
+                                    test_rotary.py, test_mrope.py; closed-form rotation
+                                    of unit vectors; relative-position invariance in
+                                    float64; planted mistakes (sign, pairing, section)
+                                    must fail.
   vision_windows.*                  135 windows / 7528 tokens / <=64 tokens per window
                                     for the 4-image grid; brute-force window enumeration.
 """

@@ -79,3 +79,24 @@ def test_workspace_size():
     assert lib.nia_paged_decode_workspace_size(64, 32, 32, 16, 128) == counters + 64 * 32 * 130 * 4
     assert lib.nia_paged_decode_workspace_size(64, 32, 512, 16, 128) == \
         counters + 64 * 32 * 16 * 130 * 4
+
+
+def test_qk_norm_rope_validation_without_launching():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails or returns first
+    args = dict(q=p, qt=1024, qh=128, k=p, kt=512, kh=128, v=p, vt=512, vh=128, qw=None, kw=None,
+                eps=1e-6, pos=p, pax=8, axes=1, inv=p, s0=0, s1=0, kc=None, vc=None, sl=None,
+                n=8, h=8, hkv=4, d=128, bs=16, nb=10, dt=0, st=None)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return lib.nia_qk_norm_rope_kv_write(*a.values())
+
+    assert call(n=0) == _lib.OK
+    assert call(n=-1) == _lib.ERR_INVALID_ARGUMENT
+    assert call(axes=2) == _lib.ERR_INVALID_ARGUMENT
+    assert call(axes=3, s0=40, s1=40) == _lib.ERR_INVALID_ARGUMENT  # sections exceed D/2
+    assert call(qw=p, kw=p, eps=-1.0) == _lib.ERR_INVALID_ARGUMENT
+    assert call(kc=p) == _lib.ERR_INVALID_ARGUMENT  # a cache write needs v_cache and slots
+    assert call(d=64) == _lib.ERR_UNSUPPORTED
+    assert call(dt=7) == _lib.ERR_UNSUPPORTED

@@ -99,7 +99,7 @@ def test_paged_layer_prefill_then_decode_matches_reference_pipeline():
     # Bit-exact at the module level: the cache equals the reference's write loop
     # applied to the k/v the module itself produced on the GPU.
     with torch.no_grad():
-        _, k_g, v_g = m._qkv(x.cuda(), md["position_ids"].cuda(), None)
+        _, k_g, v_g, _ = m._qkv(x.cuda(), md["position_ids"].cuda(), None)
     kx = torch.zeros_like(kc_g[0]).cpu()
     vx = torch.zeros_like(vc_g[0]).cpu()
     ref.kv_write_loop(k_g.cpu(), v_g.cpu(), kx, vx, md["slot_mapping"])
