@@ -7,21 +7,31 @@
 // Here each KV byte is read from HBM exactly once and shared by the G query
 // heads of its group.
 //
-// Work decomposition
-//   grid (partition, kv_head, sequence); a workgroup of 4 waves owns
-//   PART_BLOCKS consecutive KV blocks (PART_BLOCKS * BS tokens) of one
-//   (sequence, kv head) and all G query heads that read it.  Wave w takes blocks
-//   w, w + 4, w + 8, ... of the partition, double-buffering the next block's K
-//   and V in registers while it computes on the current one.
-// Lane layout inside a wave (bf16, D = 128)
-//   A block-head is BS x D contiguous elements (4 KB).  One wave-wide 16-byte
-//   load covers 1 KB: lane l gets elements [8l, 8l + 8), i.e. token l / 16 of the
-//   load and dims 8 (l % 16) .. +7.  q . k partials reduce over the 16 lanes of a
-//   token with 4 DPP adds; every lane of that row then holds the full score.
-// Softmax
+// Two kernels compute partial attention over partitions of a sequence's blocks;
+// paged_decode_combine_kernel merges the partials (one wave per (sequence, head)).
+//
+// Shapes: D = 128, BS = 16, G = H / H_kv <= 8 (others return NIA_ERR_UNSUPPORTED).
+// bf16 (the serving path)
+//   Work items are (sequence, partition of <= 32 blocks, KV head), numbered on the
+//   device from context_lens; persistent workgroups (2 per CU) take them from an
+//   atomic ticket (paged_decode_bf16_persistent_kernel), or the grid enumerates
+//   them for batches above 4096 (paged_decode_bf16_kernel).  An item's 4 waves take
+//   the partition's block pairs round-robin.  Per pair a wave issues 16 wave-wide
+//   16-byte loads (K and V of two 4 KB block-heads), and for G <= 4 the next pair's
+//   K goes out right after this pair's scores, its V right after this pair's P V.
+//   K layout: 8 lanes per token, two tokens per lane, so q . k is 8 v_dot2_f32_bf16
+//   plus a 3-step DPP sum.  V layout: 16 lanes per token (8 dims each), so P V is
+//   v_dot2_f32_bf16 over the pair's two blocks with the weights packed as a bf16
+//   pair and moved from the K lanes to the V lanes with ds_bpermute.
+// fp32 (same shapes)
+//   paged_decode_partial_kernel: grid (partition, KV head, sequence); wave w takes
+//   blocks w, w + 4, ... of the partition; 16 lanes per token in one layout for
+//   both K and V.
+// Softmax (both)
 //   Scores are kept in log2 units (scale * log2 e folded in).  Each lane row keeps
-//   its own running (m, l, o[8 dims]) over the tokens it has seen; the running max
-//   is only raised when a block's max exceeds it by more than kLazyRescale (2^8),
+//   its own running (l, o[8 dims]) against a running max (per lane row in fp32, one
+//   per wave and head in bf16) that is only raised when a block's max exceeds it
+//   by more than kLazyRescale (2^8),
 //   which keeps the O rescale off the common path and bounds p by 2^8.  At the end
 //   rows merge by shuffles, waves through LDS, partitions in the combine kernel.
 // Algorithmic HBM bytes per sequence: 2 * L * H_kv * D * s (K and V) plus q, out,
@@ -766,7 +776,7 @@ constexpr int kPersistentMaxBatch = 4096;
 // before the first call, and the last workgroup to leave returns them to zero.
 template <int G, int PART_BLOCKS>
 __global__ __launch_bounds__(kDecodeThreads)
-__attribute__((amdgpu_waves_per_eu(G <= kRollingMaxG ? 2 : 2))) void paged_decode_bf16_persistent_kernel(
+__attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
   __shared__ int s_prefix[kPersistentMaxBatch + 1];

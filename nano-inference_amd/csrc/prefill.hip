@@ -10,6 +10,11 @@
 // It also serves chunked prefill over the paged cache, which the reference
 // lacks (its prefill ignores the cache).
 //
+// Two kernels share the tiling below: prefill_dma_kernel (head_dim 64/80/96/128,
+// K/V tiles fetched by DMA into LDS; paged calls with block size >= 16 and
+// contiguous calls whose K/V token strides are below 2^26 elements) and
+// prefill_kernel (register-staged loads into a transposed V tile; the rest).
+//
 // Tiling (BLOCK_M = 128 query rows of one head per workgroup, 4 waves x 32 rows;
 // BLOCK_N = 64 keys per step)
 //   S^T = K Q^T with v_mfma_f32_32x32x16_bf16: A = K rows from LDS, B = Q^T held
@@ -18,9 +23,9 @@
 //   one lane pair (l, l ^ 32): row max and row sum need one cross-lane step.
 //   O^T = V^T P^T: the B operand (P^T) is the S^T accumulator converted to bf16
 //   in place, with the key order of each 16-key MFMA step permuted to match the
-//   accumulator layout; A (V^T) comes from a transposed V tile in LDS whose
-//   4-key groups are XOR-swizzled per row so that both the transposing writes
-//   and the operand reads spread over the LDS banks.  Every O^T register of a
+//   accumulator layout; A (V^T) is read with ds_read_b64_tr_b16 from the row-major
+//   V tile (DMA kernel), or from a transposed V tile whose 4-key groups are
+//   XOR-swizzled per row (prefill_kernel).  Every O^T register of a
 //   lane belongs to that lane's query, so rescaling O is lane-local.
 // Softmax: exp2 with scale * log2(e) folded into one FMA; the running max is only
 // raised when a tile's max exceeds it by more than 2^8 (lazy rescale).
