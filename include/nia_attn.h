@@ -197,6 +197,35 @@ int32_t nia_qk_norm_rope_kv_write(void* q, int64_t q_tok_stride, int64_t q_head_
                                   int32_t block_size, int64_t num_blocks, int32_t dtype,
                                   void* stream);
 
+/*
+ * Step metadata: the padded model inputs and attention metadata of one engine
+ * step, expanded on the device from a compact descriptor (one upload per step).
+ * Replaces the loops of src/nano_inference/engine/context_builder.py:83-193
+ * (input_ids, position_ids, context_lens, attention_mask, block tables, slot
+ * mapping) and :18-81 (mRoPE positions).
+ *   desc  int64, sections back to back:
+ *     [batch][8] headers: step_len, start_pos, num_blocks, token_offset,
+ *       block_offset, mrope_explicit e, mrope_offset, mrope_base c;
+ *     [num_tokens] step token ids; [num_blocks] block ids; [num_mrope] explicit
+ *       mRoPE rows (3 x e per sequence with e > 0).
+ *   Outputs, i < batch, j < max_step:
+ *     input_ids, position_ids, slot_mapping  [batch][max_step] int64
+ *       (0, 0, -1 past step_len; a position past the block list uses the last
+ *       block, as :176-189 does);
+ *     context_lens, last_index  [batch] int64 (start + step_len, step_len - 1);
+ *     attention_mask  [batch][max_total] bool, j < context_lens[i];
+ *     block_tables  [batch][max_blocks] int32, zero-padded;
+ *     mrope  [3][batch][max_step] int64 or NULL: explicit rows for j < e, then
+ *       c + j - e up to step_len, 0 past it.
+ * Descriptor reads are bounds-checked against the section lengths given.
+ */
+int32_t nia_step_metadata(const int64_t* desc, int64_t num_tokens, int64_t num_blocks,
+                          int64_t num_mrope, int32_t batch, int32_t max_step,
+                          int32_t max_total, int32_t max_blocks, int32_t block_size,
+                          int64_t* input_ids, int64_t* position_ids, int64_t* slot_mapping,
+                          int64_t* context_lens, int64_t* last_index, void* attention_mask,
+                          int32_t* block_tables, int64_t* mrope, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

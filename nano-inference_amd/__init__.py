@@ -10,7 +10,10 @@ with PyTorch-side layers that keep the reference engine's attention interface:
                    ``scaled_dot_product_attention`` as drop-ins for
                    src/nano_inference/layers/attention.py;
 * ``vision``     - ``VisionAttention`` (Qwen2.5-VL ViT) and its chunk producers;
-* ``context``    - ``AttentionMetadata``, field-for-field the reference's;
+* ``context``    - ``AttentionMetadata`` and ``GenerateContext``, field-for-field the
+                   reference's;
+* ``context_builder`` - ``GenerateContextBuilder``: the step's inputs and metadata
+                   built on the GPU from one upload (``nia_step_metadata``);
 * ``e2e``        - a Qwen3-architecture decoder over these layers with a paged KV
                    pool and a batched greedy generator (whole-model throughput).
 """
@@ -20,12 +23,16 @@ from .attention import (  # noqa: F401
     Qwen25VLDecoderAttention,
     scaled_dot_product_attention,
 )
-from .context import AttentionMetadata  # noqa: F401
+from .context import AttentionMetadata, GenerateContext  # noqa: F401
+from .context_builder import GenerateContextBuilder, select_last_logits  # noqa: F401
 from .vision import VisionAttention, full_cu_seqlens, window_index  # noqa: F401
 
 __all__ = [
     "ops",
     "AttentionMetadata",
+    "GenerateContext",
+    "GenerateContextBuilder",
+    "select_last_logits",
     "PagedCausalSelfAttention",
     "Qwen25VLDecoderAttention",
     "scaled_dot_product_attention",

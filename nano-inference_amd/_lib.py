@@ -62,6 +62,11 @@ SIGNATURES = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _p, _i64, _i32,
          _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p],
     ),
+    "nia_step_metadata": (
+        _i32,
+        [_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+         _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    ),
 }
 
 ABI_VERSION = 1

@@ -9,7 +9,7 @@ the reference's context builder (src/nano_inference/engine/context_builder.py:
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional
+from typing import Any, List, Optional, Tuple
 
 import torch
 
@@ -31,3 +31,21 @@ class AttentionMetadata:
 
     # VLM only: (3, B, S_step) mRoPE position ids; None for text-only batches.
     mrope_position_ids: Optional[torch.Tensor] = None
+
+
+@dataclass
+class GenerateContext:
+    """Batch-level inputs of one engine step (fields of the reference's
+    src/nano_inference/core/context.py:28-51), plus ``last_token_index``: the
+    column of each row's last real token in the padded step, where the step's
+    next-token logits must be read."""
+
+    input_ids: torch.Tensor  # (B, S_step) int64
+    attention_mask: torch.Tensor  # (B, S_total) bool
+    position_ids: torch.Tensor  # (B, S_step) int64
+    metadata: AttentionMetadata
+    request_ids: List[str]
+    token_histories: List[List[int]]
+    images: Optional[List[Any]] = None
+    image_grid_thw: Optional[List[Tuple[int, int, int]]] = None
+    last_token_index: Optional[torch.Tensor] = None  # (B,) int64

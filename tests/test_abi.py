@@ -100,3 +100,14 @@ def test_qk_norm_rope_validation_without_launching():
     assert call(kc=p) == _lib.ERR_INVALID_ARGUMENT  # a cache write needs v_cache and slots
     assert call(d=64) == _lib.ERR_UNSUPPORTED
     assert call(dt=7) == _lib.ERR_UNSUPPORTED
+
+
+def test_step_metadata_validation_without_launching():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced
+    args = [p, 10, 4, 0, 2, 5, 9, 3, 16, p, p, p, p, p, p, p, None, None]
+    assert lib.nia_step_metadata(*args[:4], 0, *args[5:]) == _lib.OK          # empty batch
+    assert lib.nia_step_metadata(*args[:4], -1, *args[5:]) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.nia_step_metadata(*args[:8], 0, *args[9:]) == _lib.ERR_INVALID_ARGUMENT  # BS 0
+    assert lib.nia_step_metadata(None, *args[1:]) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.nia_step_metadata(*args[:4], 70000, *args[5:]) == _lib.ERR_UNSUPPORTED
