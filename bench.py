@@ -223,20 +223,24 @@ def bench_decode_vl(torch, ops, workloads):
                 bytes=c.decode_bytes())
 
 
-def bench_e2e(torch):
+def bench_e2e(torch, mixed: bool):
     """Whole-model generation on the Qwen3-0.6B architecture (random-initialised bf16):
-    64 prompts of U[128, 2048] random ids, 256 greedy tokens each, decode step in a
-    HIP graph.  Throughput = (prompt + generated tokens) / elapsed."""
+    64 prompts of U[128, 2048] random ids, 256 greedy tokens each.  ``mixed``:
+    continuous batching with 1024-token prefill chunks and decodes packed into steps
+    of up to 8192 tokens, the all-decode tail in a HIP graph; otherwise prefill-first
+    (padded prefill batches of 8, then graph decode steps).  Throughput = (prompt +
+    generated tokens) / elapsed."""
     from nano_inference_amd import e2e
 
-    gen = e2e.build(use_graph=True)
+    gen = e2e.build(use_graph=True, mixed=mixed)
     gen.run([pr[:64] for pr in gen.prompts[:4]])  # warm-up
     st = gen.run(gen.prompts)
     return dict(tokens_per_s=round(st.tokens_per_s, 1),
                 decode_tokens_per_s=round(st.decode_tokens_per_s, 1),
                 prompt_tokens=st.prompt_tokens, generated_tokens=st.generated_tokens,
                 prefill_s=round(st.prefill_s, 4), decode_s=round(st.decode_s, 4),
-                total_s=round(st.total_s, 4))
+                total_s=round(st.total_s, 4), steps=st.prefill_steps + st.decode_steps,
+                scheduling="chunked prefill mixed with decodes" if mixed else "prefill first")
 
 
 def cpu_baseline(torch, workloads, budget_s: float = 20.0):
@@ -347,7 +351,8 @@ def main() -> int:
     extra["kv_write_qwen3_8b"] = dict(us=round(wr_ms * 1e3, 2),
                                       gbps=round(c.write_bytes() / (wr_ms * 1e-3) / 1e9, 1))
     if not args.no_e2e:
-        extra["e2e_qwen3_0p6b"] = bench_e2e(torch)
+        extra["e2e_qwen3_0p6b"] = bench_e2e(torch, mixed=True)
+        extra["e2e_qwen3_0p6b_prefill_first"] = bench_e2e(torch, mixed=False)
     line = {
         "metric": "decode attn HBM GB/s (% of peak) + prefill attn TFLOP/s (% bf16 MFMA peak)",
         "value": round(value, 1),

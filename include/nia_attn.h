@@ -226,6 +226,32 @@ int32_t nia_step_metadata(const int64_t* desc, int64_t num_tokens, int64_t num_b
                           int64_t* context_lens, int64_t* last_index, void* attention_mask,
                           int32_t* block_tables, int64_t* mrope, void* stream);
 
+/*
+ * Packed step metadata for batches that mix prefill chunks and decodes (no
+ * counterpart in the reference, whose batches are all-prefill or all-decode,
+ * src/nano_inference/scheduler/scheduler.py:176-230): the same expansion as
+ * nia_step_metadata, with the step's tokens back to back instead of padded.
+ *   desc  int64: [batch][8] headers (step_len, start_pos, num_blocks,
+ *     token_offset, block_offset, out_offset, device_token_index, 0), then
+ *     [num_tokens] token ids, then [num_blocks] block ids.
+ *   A sequence with device_token_index >= 0 reads its step tokens from
+ *   device_tokens[device_token_index + j] (tokens sampled on the device).
+ *   Outputs: input_ids, position_ids, slot_mapping [num_rows] int64 at rows
+ *     out_offset + j (num_rows = total step tokens; rows outside are not written); context_lens [batch] int64;
+ *     last_index [batch] int64 (out_offset + step_len - 1); q_start, q_len
+ *     [batch] int32 (out_offset, step_len: the varlen description nia_prefill_paged
+ *     takes); block_tables [batch][max_blocks] int32, zero-padded.
+ * Descriptor and device-token reads are bounds-checked against the lengths given.
+ */
+int32_t nia_step_metadata_packed(const int64_t* desc, int64_t num_tokens, int64_t num_blocks,
+                                 const int64_t* device_tokens, int64_t num_device_tokens,
+                                 int32_t batch, int64_t num_rows, int32_t max_step,
+                                 int32_t max_blocks,
+                                 int32_t block_size, int64_t* input_ids, int64_t* position_ids,
+                                 int64_t* slot_mapping, int64_t* context_lens,
+                                 int64_t* last_index, int32_t* q_start, int32_t* q_len,
+                                 int32_t* block_tables, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,11 @@ SIGNATURES = {
         [_p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
          _p, _p, _p, _p, _p, _p, _p, _p, _p],
     ),
+    "nia_step_metadata_packed": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i32, _i64, _i32, _i32, _i32,
+         _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    ),
 }
 
 ABI_VERSION = 1

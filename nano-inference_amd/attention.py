@@ -9,10 +9,13 @@ the reference's src/nano_inference/layers/attention.py:
   ``forward(x, position_ids, attention_mask=None, metadata=None)``;
 * ``Qwen25VLDecoderAttention`` (:343-371), the mRoPE variant.
 
-Projections, QK-RMSNorm and RoPE stay PyTorch ops, as in the reference; the
-KV-cache write, the block-table gather, GQA, masking and softmax attention run
-in the HIP kernels.  Differences from the reference, all where the reference
-has no defined behaviour of its own:
+Projections stay PyTorch ops, as in the reference.  QK-RMSNorm, RoPE / mRoPE and
+the KV-cache write run as one fused kernel (head_dim 128; other head dims keep the
+PyTorch norm and rotary ops and the plain write kernel), and the block-table
+gather, GQA, masking and softmax attention run in the attention kernels.  A
+``PackedAttentionMetadata`` step (decodes and prefill chunks in one packed row)
+splits its rows between the decode and the chunked-prefill kernel.  Differences
+from the reference, all where the reference has no defined behaviour of its own:
 * a decode step (``is_prefill`` False) with more than one new token per
   sequence attends with a bottom-right causal mask (chunked prefill); the
   reference applies no causal mask when S_q != S_k
@@ -29,7 +32,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .context import AttentionMetadata
+from .context import AttentionMetadata, PackedAttentionMetadata
 from .layers import MRotaryEmbedding, RMSNorm, RotaryEmbedding
 
 
@@ -213,7 +216,9 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         if not written and k_cache is not None and metadata.slot_mapping is not None:
             ops.kv_write(k, v, k_cache, v_cache, metadata.slot_mapping)
 
-        if metadata.is_prefill:
+        if isinstance(metadata, PackedAttentionMetadata):
+            attn = self._packed_attention(q, k_cache, v_cache, metadata)
+        elif metadata.is_prefill:
             # 2a. Prefill attends over the step's fresh K/V (:281-284).  Padded
             # rows past a sequence's length see all its keys, as in the reference.
             attn = self._dense_causal(q, k, v, attention_mask)
@@ -237,6 +242,26 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         else:
             attn = self._dense_causal(q, k, v, attention_mask)
         return self.o_proj(attn.reshape(b, s, self.num_heads * self.head_dim))
+
+
+    def _packed_attention(self, q, k_cache, v_cache, md: PackedAttentionMetadata):
+        """Decode rows through the decode kernel, chunk rows through the chunked
+        prefill kernel, both reading the paged cache the step has just written."""
+        if k_cache is None:
+            raise ValueError("a packed step needs the KV cache")
+        t = q.shape[0] * q.shape[1]
+        q2 = q.reshape(t, self.num_heads, self.head_dim)
+        out = torch.empty_like(q2)
+        nd = md.num_decode
+        n = md.q_start.shape[0]
+        if nd > 0:
+            ops.paged_decode(q2[:nd], k_cache, v_cache, md.kv_block_tables[:nd],
+                             md.context_lens[:nd], out=out[:nd])
+        if nd < n:
+            ops.prefill_paged(q2, k_cache, v_cache, md.kv_block_tables[nd:], md.q_start[nd:],
+                              md.q_len[nd:], md.context_lens[nd:], md.max_q_len,
+                              ops.CAUSAL_BOTTOM_RIGHT, out=out)
+        return out
 
 
 class Qwen25VLDecoderAttention(PagedCausalSelfAttention):

@@ -49,3 +49,18 @@ class GenerateContext:
     images: Optional[List[Any]] = None
     image_grid_thw: Optional[List[Tuple[int, int, int]]] = None
     last_token_index: Optional[torch.Tensor] = None  # (B,) int64
+
+
+@dataclass
+class PackedAttentionMetadata(AttentionMetadata):
+    """A step whose tokens lie back to back in one row, (1, T): sequences
+    0 .. num_decode - 1 feed one token each (rows 0 .. num_decode - 1) and decode;
+    the others feed a prefill chunk of q_len[s] rows from row q_start[s], on top of
+    the context_lens[s] - q_len[s] tokens already cached.  Lets one step mix prefill
+    chunks and decodes; the reference's batches are all-prefill or all-decode
+    (src/nano_inference/scheduler/scheduler.py:176-230)."""
+
+    q_start: Optional[torch.Tensor] = None  # (B,) int32
+    q_len: Optional[torch.Tensor] = None  # (B,) int32
+    num_decode: int = 0
+    max_q_len: int = 0

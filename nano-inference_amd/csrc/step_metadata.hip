@@ -95,6 +95,61 @@ __global__ __launch_bounds__(kMetaThreads) void step_metadata_kernel(MetaParams 
   }
 }
 
+// Packed layout: the step's tokens back to back (no padding), for batches that mix
+// prefill chunks and decodes.  Header words 5 and 6 are the sequence's first row
+// in the packed outputs and a device token index (or -1): with an index, the
+// step's tokens are read from device_tokens[index + j] (decode tokens sampled on
+// the device, never seen by the host).
+struct PackedParams {
+  const int64_t* desc;
+  int64_t num_tokens, num_blocks;
+  const int64_t* device_tokens;
+  int64_t num_device_tokens;
+  int64_t num_rows;        // T
+  int32_t batch, max_step, max_blocks, block_size;
+  int64_t* input_ids;      // [T]
+  int64_t* position_ids;   // [T]
+  int64_t* slot_mapping;   // [T]
+  int64_t* context_lens;   // [batch]
+  int64_t* last_index;     // [batch]: packed row of the sequence's last token
+  int32_t* q_start;        // [batch]
+  int32_t* q_len;          // [batch]
+  int32_t* block_tables;   // [batch][max_blocks]
+};
+
+__global__ __launch_bounds__(kMetaThreads) void step_metadata_packed_kernel(PackedParams p) {
+  const int i = blockIdx.y;
+  const int j = blockIdx.x * kMetaThreads + threadIdx.x;
+  const int64_t* h = p.desc + (int64_t)i * kHeaderWords;
+  const int64_t step_len = h[0], start = h[1], nblk = h[2], tok_off = h[3], blk_off = h[4];
+  const int64_t out_off = h[5], src = h[6];
+  const int64_t* tokens = p.desc + (int64_t)p.batch * kHeaderWords;
+  const int64_t* blocks = tokens + p.num_tokens;
+  if (j < step_len && j < p.max_step && out_off + j >= 0 && out_off + j < p.num_rows) {
+    const int64_t t = out_off + j;
+    const int64_t pos = start + j;
+    p.input_ids[t] = src >= 0 ? load_or_zero(p.device_tokens, src + j, p.num_device_tokens)
+                              : load_or_zero(tokens, tok_off + j, p.num_tokens);
+    p.position_ids[t] = pos;
+    int64_t slot = -1;
+    if (nblk > 0) {
+      const int64_t bi = pos / p.block_size;
+      const int64_t phys = load_or_zero(blocks, blk_off + (bi < nblk ? bi : nblk - 1), p.num_blocks);
+      slot = phys * p.block_size + (pos - bi * p.block_size);
+    }
+    p.slot_mapping[t] = slot;
+  }
+  if (j < p.max_blocks)
+    p.block_tables[(int64_t)i * p.max_blocks + j] =
+        j < nblk ? (int32_t)load_or_zero(blocks, blk_off + j, p.num_blocks) : 0;
+  if (j == 0) {
+    p.context_lens[i] = start + step_len;
+    p.last_index[i] = out_off + step_len - 1;
+    p.q_start[i] = (int32_t)out_off;
+    p.q_len[i] = (int32_t)step_len;
+  }
+}
+
 }  // namespace
 
 extern "C" int32_t nia_step_metadata(
@@ -136,5 +191,49 @@ extern "C" int32_t nia_step_metadata(
   p.mrope = mrope;
   const dim3 grid((unsigned)((width + kMetaThreads - 1) / kMetaThreads), (unsigned)batch);
   hipLaunchKernelGGL(step_metadata_kernel, grid, dim3(kMetaThreads), 0, (hipStream_t)stream, p);
+  return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+}
+
+extern "C" int32_t nia_step_metadata_packed(
+    const int64_t* desc, int64_t num_tokens, int64_t num_blocks, const int64_t* device_tokens,
+    int64_t num_device_tokens, int32_t batch, int64_t num_rows, int32_t max_step,
+    int32_t max_blocks, int32_t block_size, int64_t* input_ids, int64_t* position_ids, int64_t* slot_mapping,
+    int64_t* context_lens, int64_t* last_index, int32_t* q_start, int32_t* q_len,
+    int32_t* block_tables, void* stream) {
+  if (batch < 0 || num_rows < 0 || max_step < 0 || max_blocks < 0 || num_tokens < 0 ||
+      num_blocks < 0 || num_device_tokens < 0)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return NIA_OK;
+  if (block_size <= 0 || !desc || !context_lens || !last_index || !q_start || !q_len)
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (num_rows > 0 && (!input_ids || !position_ids || !slot_mapping))
+    return NIA_ERR_INVALID_ARGUMENT;
+  if (max_blocks > 0 && !block_tables) return NIA_ERR_INVALID_ARGUMENT;
+  if (num_device_tokens > 0 && !device_tokens) return NIA_ERR_INVALID_ARGUMENT;
+  if (batch > 65535) return NIA_ERR_UNSUPPORTED;
+  int width = max_step > max_blocks ? max_step : max_blocks;
+  if (width < 1) width = 1;
+  PackedParams p{};
+  p.desc = desc;
+  p.num_tokens = num_tokens;
+  p.num_blocks = num_blocks;
+  p.device_tokens = device_tokens;
+  p.num_device_tokens = num_device_tokens;
+  p.num_rows = num_rows;
+  p.batch = batch;
+  p.max_step = max_step;
+  p.max_blocks = max_blocks;
+  p.block_size = block_size;
+  p.input_ids = input_ids;
+  p.position_ids = position_ids;
+  p.slot_mapping = slot_mapping;
+  p.context_lens = context_lens;
+  p.last_index = last_index;
+  p.q_start = q_start;
+  p.q_len = q_len;
+  p.block_tables = block_tables;
+  const dim3 grid((unsigned)((width + kMetaThreads - 1) / kMetaThreads), (unsigned)batch);
+  hipLaunchKernelGGL(step_metadata_packed_kernel, grid, dim3(kMetaThreads), 0,
+                     (hipStream_t)stream, p);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }

@@ -45,7 +45,7 @@ import torch.nn.functional as F
 
 from . import ops
 from .attention import PagedCausalSelfAttention
-from .context import AttentionMetadata
+from .context import AttentionMetadata, PackedAttentionMetadata
 from .layers import RMSNorm
 
 
@@ -128,6 +128,15 @@ class Qwen3ForCausalLM(nn.Module):
             x = layer(x, position_ids, attention_mask, metadata)
         last = x[torch.arange(x.shape[0], device=x.device), select]
         return self.lm_head(self.norm(last))
+
+
+    def forward_packed(self, input_ids, position_ids, metadata, rows):
+        """A packed step: input_ids / position_ids (T,), logits at packed ``rows``."""
+        x = self.embed_tokens(input_ids).unsqueeze(0)
+        pos = position_ids.unsqueeze(0)
+        for layer in self.layers:
+            x = layer(x, pos, None, metadata)
+        return self.lm_head(self.norm(x[0, rows]))
 
 
 class KVPool:
@@ -305,6 +314,270 @@ class Generator:
         self._step += 1
 
 
+@dataclass
+class StepEntry:
+    """One sequence's part of a step: ``n`` tokens from position ``start``; a decode
+    feeds the token it sampled last; ``sample`` is the index of the token the step
+    samples for it (None: a chunk that does not finish the prompt)."""
+
+    sid: int
+    start: int
+    n: int
+    decode: bool
+    sample: Optional[int]
+
+
+class ChunkedScheduler:
+    """Host-side plan of continuous batching with chunked prefill (lengths only).
+
+    Each step takes one token from every decoding sequence first, then prefill
+    chunks of at most ``chunk`` tokens from sequences still reading their prompt,
+    in admission order, up to ``max_step_tokens`` in all; waiting prompts are
+    admitted (``admit(sid)`` is called) while the step has room.  A chunk that
+    ends its prompt samples the first token; a sequence leaves after
+    ``max_new`` tokens (``leave(sid)``).
+    """
+
+    def __init__(self, prompt_lens: List[int], max_new: int, max_step_tokens: int, chunk: int,
+                 admit=None, leave=None):
+        if max_new < 1 or chunk < 1 or max_step_tokens < 1:
+            raise ValueError("max_new, chunk and max_step_tokens must be positive")
+        self.lens = list(prompt_lens)
+        self.max_new = max_new
+        self.max_step_tokens = max_step_tokens
+        self.chunk = chunk
+        self.admit = admit or (lambda sid: None)
+        self.leave = leave or (lambda sid: None)
+        self.waiting = deque(range(len(self.lens)))
+        self.filling: List[int] = []
+        self.decoding: List[int] = []
+        self.cached = [0] * len(self.lens)
+        self.produced = [0] * len(self.lens)
+
+    def done(self) -> bool:
+        return not (self.waiting or self.filling or self.decoding)
+
+    def _next_chunk(self, sid: int, budget: int) -> int:
+        return min(self.chunk, self.lens[sid] - self.cached[sid], budget)
+
+    def plan(self) -> List[StepEntry]:
+        room = self.max_step_tokens - len(self.decoding) - sum(
+            self._next_chunk(sid, self.max_step_tokens) for sid in self.filling)
+        while self.waiting and room > 0:
+            sid = self.waiting.popleft()
+            self.admit(sid)
+            self.filling.append(sid)
+            room -= self._next_chunk(sid, self.max_step_tokens)
+        out = [StepEntry(sid, self.lens[sid] + self.produced[sid] - 1, 1, True,
+                         self.produced[sid]) for sid in self.decoding]
+        budget = self.max_step_tokens - len(self.decoding)
+        for sid in self.filling:
+            if budget <= 0:
+                break
+            n = self._next_chunk(sid, budget)
+            ends = self.cached[sid] + n == self.lens[sid]
+            out.append(StepEntry(sid, self.cached[sid], n, False, 0 if ends else None))
+            budget -= n
+        return out
+
+    def commit(self, step: List[StepEntry]) -> None:
+        for e in step:
+            if e.decode:
+                self.produced[e.sid] += 1
+            else:
+                self.cached[e.sid] += e.n
+                if self.cached[e.sid] == self.lens[e.sid]:
+                    self.produced[e.sid] = 1
+        still = []
+        for sid in self.decoding:
+            (self.leave(sid) if self.produced[sid] >= self.max_new else still.append(sid))
+        for sid in [sid for sid in self.filling if self.cached[sid] == self.lens[sid]]:
+            self.filling.remove(sid)
+            (self.leave(sid) if self.produced[sid] >= self.max_new else still.append(sid))
+        self.decoding = still
+
+
+class MixedGenerator:
+    """Continuous batching with chunked prefill over the attention path: each step
+    of ``ChunkedScheduler`` runs as one packed row of tokens, decodes first, with
+    ``PackedAttentionMetadata`` (one decode launch for the decode rows, one
+    chunked-prefill launch over the paged cache for the chunk rows).
+
+    A step's metadata is one descriptor upload expanded on the device
+    (``nia_step_metadata_packed``).  Sampled tokens stay on the device and the next
+    step reads them from there, so no step waits for the host.  Once no prompt is
+    left to read, the remaining decode steps replay one captured HIP graph.
+    Stats: ``prefill_steps`` counts the packed steps (mixed or not), ``prefill_s``
+    the time until every prompt is in the cache.
+    """
+
+    def __init__(self, model: Qwen3ForCausalLM, pool: KVPool, max_new_tokens: int,
+                 max_step_tokens: int = 8192, chunk: int = 1024, use_graph: bool = True):
+        self.model = model
+        self.pool = pool
+        self.max_new = max_new_tokens
+        self.max_step_tokens = max_step_tokens
+        self.chunk = chunk
+        self.use_graph = use_graph
+        self.replay_hook = None  # called after every graph replay (tests interleave work)
+        self.device = pool.k_cache.device
+
+    def _decode_tail(self, sched: "ChunkedScheduler", host_blocks, prompts, st) -> None:
+        """Once every sequence decodes, the remaining steps have one shape: feed each
+        sequence's last token, sample the next.  They run as replays of one captured
+        HIP graph; a sequence that has its max_new tokens keeps recomputing its last
+        position (same slot, same values) and writes its sample to a spare entry."""
+        import numpy as np
+
+        dev = self.device
+        sids = list(sched.decoding)
+        b = len(sids)
+        left = max(self.max_new - sched.produced[sid] for sid in sids)
+        width = max(len(host_blocks[sid]) for sid in sids)
+        bt = np.zeros((b, width), dtype=np.int32)
+        for i, sid in enumerate(sids):
+            bt[i, :len(host_blocks[sid])] = host_blocks[sid]
+        self._bt = torch.from_numpy(bt).to(dev)
+        self._sid = torch.tensor(sids, dtype=torch.int64, device=dev)
+        self._plen = torch.tensor([len(prompts[sid]) for sid in sids], dtype=torch.int64,
+                                  device=dev)
+        self._prod = torch.tensor([sched.produced[sid] for sid in sids], dtype=torch.int64,
+                                  device=dev)
+        self._rows = torch.arange(b, device=dev)
+        self._zero = torch.zeros(b, dtype=torch.int64, device=dev)
+        self._spare = torch.full((b,), self._tok.numel() - 1, dtype=torch.int64, device=dev)
+        self._tail_step()
+        st.decode_steps += 1
+        if left > 1:
+            if self.use_graph and left > 2:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    self._tail_step()
+                for _ in range(left - 1):
+                    graph.replay()
+                    st.decode_steps += 1
+                    if self.replay_hook is not None:
+                        self.replay_hook()
+            else:
+                for _ in range(left - 1):
+                    self._tail_step()
+                    st.decode_steps += 1
+        for sid in sids:
+            sched.produced[sid] = self.max_new
+            sched.leave(sid)
+        sched.decoding = []
+
+    def _tail_step(self) -> None:
+        bs = self.pool.block_size
+        last = self._prod - 1
+        p = self._plen + last
+        tok = self._tok[self._sid * self.max_new + last]
+        slot = self._bt[self._rows, p // bs].to(torch.int64) * bs + p % bs
+        md = AttentionMetadata(context_lens=p + 1, kv_block_tables=self._bt,
+                               slot_mapping=slot.unsqueeze(1), k_cache=self.pool.k_cache,
+                               v_cache=self.pool.v_cache, is_prefill=False)
+        logits = self.model(tok.unsqueeze(1), p.unsqueeze(1), None, md, self._zero)
+        live = self._prod < self.max_new
+        dst = torch.where(live, self._sid * self.max_new + self._prod, self._spare)
+        self._tok.index_put_((dst,), torch.argmax(logits, dim=-1))
+        self._prod += live.to(torch.int64)
+
+    @torch.no_grad()
+    def run(self, prompts: List[List[int]]) -> GenerationStats:
+        import numpy as np
+
+        from . import _lib
+
+        st = GenerationStats(prompt_tokens=sum(len(p) for p in prompts))
+        dev = self.device
+        n_seq = len(prompts)
+        # one spare entry at the end takes the samples of finished sequences
+        self._tok = torch.zeros(n_seq * self.max_new + 1, dtype=torch.int64, device=dev)
+        blocks: Dict[int, List[int]] = {}
+        host_blocks: Dict[int, np.ndarray] = {}
+
+        def admit(sid):
+            blocks[sid] = self.pool.allocate(len(prompts[sid]) + self.max_new)
+            host_blocks[sid] = np.asarray(blocks[sid], dtype=np.int64)
+
+        def leave(sid):
+            self.pool.release(blocks.pop(sid))
+
+        sched = ChunkedScheduler([len(p) for p in prompts], self.max_new, self.max_step_tokens,
+                                 self.chunk, admit, leave)
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        bs = self.pool.block_size
+        i64 = dict(dtype=torch.int64, device=dev)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        t1 = None
+        while not sched.done():
+            if not sched.waiting and not sched.filling:
+                if t1 is None:
+                    torch.cuda.synchronize(dev)
+                    t1 = time.perf_counter()
+                self._decode_tail(sched, host_blocks, prompts, st)
+                break
+            step = sched.plan()
+            b, t = len(step), sum(e.n for e in step)
+            nd = sum(1 for e in step if e.decode)
+            hdr = np.zeros((b, 8), dtype=np.int64)
+            host_tok, tables_h = [], []
+            sample_row, sample_slot = [], []
+            tok_off = blk_off = out_off = 0
+            for i, e in enumerate(step):
+                bl = host_blocks[e.sid]
+                src = e.sid * self.max_new + e.sample - 1 if e.decode else -1
+                hdr[i] = (e.n, e.start, len(bl), tok_off, blk_off, out_off, src, 0)
+                if not e.decode:
+                    host_tok.append(np.asarray(prompts[e.sid][e.start:e.start + e.n],
+                                               dtype=np.int64))
+                    tok_off += e.n
+                tables_h.append(bl)
+                blk_off += len(bl)
+                out_off += e.n
+                if e.sample is not None:
+                    sample_row.append(i)
+                    sample_slot.append(e.sid * self.max_new + e.sample)
+            ns = len(sample_row)
+            desc = np.concatenate([hdr.reshape(-1)] + host_tok + tables_h +
+                                  [np.asarray(sample_row + sample_slot, dtype=np.int64)])
+            d = torch.from_numpy(desc).pin_memory().to(dev, non_blocking=True)
+            max_blocks = max(len(x) for x in tables_h)
+            max_step = max(e.n for e in step)
+            ids, pos, slots = (torch.empty(t, **i64) for _ in range(3))
+            ctx, last = torch.empty(b, **i64), torch.empty(b, **i64)
+            q_start = torch.empty(b, dtype=torch.int32, device=dev)
+            q_len = torch.empty(b, dtype=torch.int32, device=dev)
+            tables = torch.empty((b, max_blocks), dtype=torch.int32, device=dev)
+            rc = lib.nia_step_metadata_packed(
+                d.data_ptr(), tok_off, blk_off, self._tok.data_ptr(), self._tok.numel(), b, t,
+                max_step, max_blocks, bs, ids.data_ptr(), pos.data_ptr(), slots.data_ptr(),
+                ctx.data_ptr(), last.data_ptr(), q_start.data_ptr(), q_len.data_ptr(),
+                tables.data_ptr(), stream)
+            _lib.check("nia_step_metadata_packed", rc)
+            md = PackedAttentionMetadata(
+                context_lens=ctx, kv_block_tables=tables, slot_mapping=slots.unsqueeze(0),
+                k_cache=self.pool.k_cache, v_cache=self.pool.v_cache, is_prefill=nd < b,
+                q_start=q_start, q_len=q_len, num_decode=nd,
+                max_q_len=max((e.n for e in step[nd:]), default=1))
+            tail = d[desc.size - 2 * ns:]
+            logits = self.model.forward_packed(ids, pos, md, last[tail[:ns]])
+            if ns:
+                self._tok[tail[ns:]] = torch.argmax(logits, dim=-1)
+            sched.commit(step)
+            st.prefill_steps += 1
+        torch.cuda.synchronize(dev)
+        t2 = time.perf_counter()
+        t1 = t2 if t1 is None else t1
+        st.generated_tokens = n_seq * self.max_new
+        st.prefill_s, st.decode_s, st.total_s = t1 - t0, t2 - t1, t2 - t0
+        out = self._tok[:n_seq * self.max_new].view(n_seq, self.max_new).cpu()
+        self.outputs = [out[i].tolist() for i in range(n_seq)]
+        return st
+
+
 def config4_prompts(num_requests: int = 64, lo: int = 128, hi: int = 2048,
                     vocab: int = 151936, seed: int = 4004) -> List[List[int]]:
     """64 prompts of U[128, 2048] token ids drawn U[0, vocab), seeded."""
@@ -316,14 +589,21 @@ def config4_prompts(num_requests: int = 64, lo: int = 128, hi: int = 2048,
 def build(cfg: Optional[Qwen3Config] = None, prompts: Optional[List[List[int]]] = None,
           max_new_tokens: int = 256, block_size: int = 16, max_prefill_batch: int = 8,
           device: str = "cuda", dtype=torch.bfloat16, seed: int = 4004,
-          use_graph: bool = False) -> Generator:
-    """Random-initialised model, a KV pool sized for the prompts, and a Generator."""
+          use_graph: bool = False, mixed: bool = False, max_step_tokens: int = 8192,
+          chunk: int = 1024):
+    """Random-initialised model, a KV pool sized for the prompts, and a generator:
+    ``MixedGenerator`` (chunked prefill mixed with decodes) when ``mixed``, else the
+    prefill-first ``Generator``."""
     cfg = cfg or Qwen3Config()
     prompts = prompts if prompts is not None else config4_prompts(seed=seed)
     model = Qwen3ForCausalLM(cfg).init_random(seed).to(device=device, dtype=dtype).eval()
     need = sum(math.ceil((len(p) + max_new_tokens) / block_size) for p in prompts)
     pool = KVPool(cfg, need + 16, block_size, dtype, torch.device(device))
-    gen = Generator(model, pool, max_new_tokens, max_prefill_batch, use_graph=use_graph)
+    if mixed:
+        gen = MixedGenerator(model, pool, max_new_tokens, max_step_tokens, chunk,
+                             use_graph=use_graph)
+    else:
+        gen = Generator(model, pool, max_new_tokens, max_prefill_batch, use_graph=use_graph)
     gen.prompts = prompts
     return gen
 
@@ -384,10 +664,15 @@ def main() -> int:
     ap.add_argument("--prefill-batch", type=int, default=8)
     ap.add_argument("--time-attention", action="store_true")
     ap.add_argument("--eager", action="store_true", help="no HIP graph for the decode step")
+    ap.add_argument("--mixed", action="store_true",
+                    help="continuous batching with chunked prefill mixed with decodes")
+    ap.add_argument("--step-tokens", type=int, default=8192)
+    ap.add_argument("--chunk", type=int, default=1024)
     args = ap.parse_args()
     cfg = Qwen3Config(num_layers=args.layers)
     gen = build(cfg, config4_prompts(args.requests), args.max_new_tokens,
-                max_prefill_batch=args.prefill_batch, use_graph=not args.eager)
+                max_prefill_batch=args.prefill_batch, use_graph=not args.eager,
+                mixed=args.mixed, max_step_tokens=args.step_tokens, chunk=args.chunk)
     gen.run([p[:64] for p in gen.prompts[:4]])  # warm-up: kernels, allocator, workspaces
     st = gen.run(gen.prompts)
     line = {"tokens_per_s": round(st.tokens_per_s, 1),
@@ -397,7 +682,7 @@ def main() -> int:
             "total_s": round(st.total_s, 4), "prefill_steps": st.prefill_steps,
             "decode_steps": st.decode_steps}
     if args.time_attention:  # eager, so that every call is timed on its own
-        gen.use_graph = False
+        gen.use_graph = False  # (the mixed generator has no graph)
         with AttentionTimer(gen.model) as tm:
             gen.run(gen.prompts)
         line.update({k: round(v, 4) for k, v in tm.totals_ms().items()})

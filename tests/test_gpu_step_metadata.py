@@ -82,3 +82,61 @@ def test_last_token_select():
     logits = torch.arange(2 * 7 * 4, dtype=torch.float32, device="cuda").view(2, 7, 4)
     sel = select_last_logits(logits, ctx)
     assert torch.equal(sel.cpu(), torch.stack([logits[0, 6], logits[1, 2]]).cpu())
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_packed_layout_matches_padded_rows(seed):
+    """nia_step_metadata_packed: row out_offset + j of every packed output equals
+    column j of the padded oracle tensors; q_start / q_len / last_index describe the
+    packing; a sequence with a device token index reads its token from there."""
+    import numpy as np
+
+    from nano_inference_amd import _lib
+
+    qs = random_batch(300 + seed, 11, block_size=16 if seed % 2 else 4, short_tables=seed >= 2)
+    exp = meta.build_context([to_oracle(q) for q in qs])
+    steps = [exp["input_ids"][i, :int((exp["slot_mapping"][i] >= 0).sum())].tolist()
+             for i in range(len(qs))]
+    dev_tok = torch.arange(1000, 1100, dtype=torch.int64, device="cuda")
+    hdr, toks, blks = [], [], []
+    tok_off = blk_off = out_off = 0
+    for i, (q, st) in enumerate(zip(qs, steps)):
+        n = len(st)
+        start = int(exp["position_ids"][i, 0])
+        bl = q.kv_cache_block.block_ids
+        src = 7 * i if n == 1 and i % 2 == 0 else -1  # some decodes read a device token
+        hdr.append([n, start, len(bl), tok_off, blk_off, out_off, src, 0])
+        if src < 0:
+            toks += st
+            tok_off += n
+        blks += bl
+        blk_off += len(bl)
+        out_off += n
+    b, t = len(qs), out_off
+    desc = torch.tensor(np.concatenate([np.asarray(hdr, np.int64).reshape(-1),
+                                        np.asarray(toks, np.int64), np.asarray(blks, np.int64)]),
+                        device="cuda")
+    mb = exp["kv_block_tables"].shape[1]
+    i64 = dict(dtype=torch.int64, device="cuda")
+    ids, pos, slots = (torch.full((t,), -7, **i64) for _ in range(3))
+    ctx, last = torch.empty(b, **i64), torch.empty(b, **i64)
+    qst = torch.empty(b, dtype=torch.int32, device="cuda")
+    qln = torch.empty(b, dtype=torch.int32, device="cuda")
+    tables = torch.empty((b, mb), dtype=torch.int32, device="cuda")
+    rc = _lib.load().nia_step_metadata_packed(
+        desc.data_ptr(), tok_off, blk_off, dev_tok.data_ptr(), dev_tok.numel(), b, t,
+        max(len(s) for s in steps), mb, qs[0].kv_cache_block.block_size, ids.data_ptr(),
+        pos.data_ptr(), slots.data_ptr(), ctx.data_ptr(), last.data_ptr(), qst.data_ptr(),
+        qln.data_ptr(), tables.data_ptr(), None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    ids, pos, slots = ids.cpu(), pos.cpu(), slots.cpu()
+    assert torch.equal(ctx.cpu(), exp["context_lens"])
+    assert torch.equal(tables.cpu(), exp["kv_block_tables"])
+    for i, (h, st) in enumerate(zip(hdr, steps)):
+        n, o = h[0], h[5]
+        want_ids = [1000 + h[6]] if h[6] >= 0 else st
+        assert ids[o:o + n].tolist() == want_ids, i
+        assert torch.equal(pos[o:o + n], exp["position_ids"][i, :n]), i
+        assert torch.equal(slots[o:o + n], exp["slot_mapping"][i, :n]), i
+        assert int(qst[i]) == o and int(qln[i]) == n and int(last[i]) == o + n - 1
