@@ -766,58 +766,121 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_bf16_kernel(Decod
 // per-sequence partition counts).
 constexpr int kPersistentMaxBatch = 4096;
 
+// Inclusive prefix sum over the lanes of a wave.
+NIA_DEVICE int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Exclusive prefix sum of v over the workgroup's threads, and the total.  Every
+// thread must call it (it holds two barriers); s_wave has one slot per wave.
+NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int inc = wave_inclusive_scan(v, lane);
+  if (lane == kWave - 1) s_wave[wave] = inc;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kDecodeWaves; ++w) {
+    const int sw = s_wave[w];
+    base += w < wave ? sw : 0;
+    tot += sw;
+  }
+  total = tot;
+  __syncthreads();
+  return base + inc - v;
+}
+
 // Persistent variant: a grid of as many workgroups as the chip holds at once.
-// Work items are (sequence, partition, KV head) in that order, numbered on the
-// device from context_lens; workgroups take them from an atomic ticket counter
-// (the next ticket is requested while the current item runs), so the grid
-// never carries empty workgroups and a short item is followed at once by the
-// next.  Partials go to paged_decode_combine_kernel, launched after this one.
-// The two counters live at the start of the workspace: they must be zero
-// before the first call, and the last workgroup to leave returns them to zero.
+// Work items are (sequence, partition, KV head), numbered on the device from
+// context_lens; workgroup w starts with item w and then takes items from an
+// atomic ticket counter (the next ticket is requested while the current item
+// runs), so the grid never carries empty workgroups and a short item is
+// followed at once by the next.
+// Sequences enter the queue in decreasing order of their item size (blocks per
+// partition), so the last tickets are the shortest items and the workgroups
+// finish close together.  Partials go to paged_decode_combine_kernel, launched
+// after this one.  The two counters live at the start of the workspace: they
+// must be zero before the first call, and the last workgroup to leave returns
+// them to zero.
 template <int G, int PART_BLOCKS>
 __global__ __launch_bounds__(kDecodeThreads)
 __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
-  __shared__ int s_prefix[kPersistentMaxBatch + 1];
-  __shared__ int s_scan[kDecodeThreads];
+  constexpr int kBins = PART_BLOCKS + 1;  // item sizes 0 (no keys) .. PART_BLOCKS
+  static_assert(kBins <= kWave, "one wave scans the size bins");
+  __shared__ int s_prefix[kPersistentMaxBatch + 1];  // work order: first item of each sequence
+  __shared__ int s_order[kPersistentMaxBatch];       // work order -> sequence
+  __shared__ int s_bins[kBins];
+  __shared__ int s_wave[kDecodeWaves];
   __shared__ int s_ticket[2];
   const int tid = threadIdx.x;
   const int64_t cap = (int64_t)p.max_blocks * BS;
 
-  // First ticket goes out before the index is built.
-  if (tid == 0) s_ticket[0] = atomicAdd(&counters[0], 1);
+  // The first item is the workgroup's own id; later tickets come from the counter,
+  // offset by the grid size.  (All workgroups asking one counter at launch would
+  // queue on it for about 10 us before any KV load.)
+  if (tid == 0) s_ticket[0] = blockIdx.x;
 
-  // ---- partitions per sequence and their exclusive prefix sums ------------------------
-  // Thread t owns sequences [t * kPer, t * kPer + kPer): one pass for its sum,
-  // a workgroup scan, a second pass to write the prefixes.
+  // ---- work index -------------------------------------------------------------------------
+  // Thread t owns sequences [t * kPer, t * kPer + kPer); their context lengths are
+  // loaded together, once.  A counting sort over the item size (bins in LDS) gives
+  // the work order, then a workgroup scan the first item number of each sequence.
   constexpr int kPer = (kPersistentMaxBatch + kDecodeThreads - 1) / kDecodeThreads;
-  auto parts_of = [&](int bi) -> int {
-    int64_t c = p.context_lens[bi];
+  const int b0 = tid * kPer;
+  int nparts[kPer], bin[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    int64_t c = b0 + k < batch ? p.context_lens[b0 + k] : 0;
     c = c < 0 ? 0 : (c > cap ? cap : c);
     const int blocks = (int)((c + BS - 1) / BS);
-    return blocks > 0 ? (blocks + PART_BLOCKS - 1) / PART_BLOCKS : 1;  // 1 zero-fill item
-  };
-  const int b0 = tid * kPer;
-  const int b1 = min(b0 + kPer, batch);
+    nparts[k] = blocks > 0 ? (blocks + PART_BLOCKS - 1) / PART_BLOCKS : 1;  // 1 zero-fill item
+    bin[k] = PART_BLOCKS - (blocks + nparts[k] - 1) / nparts[k];  // bin 0 = largest items
+  }
+  if (tid < kBins) s_bins[tid] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (b0 + k < batch) atomicAdd(&s_bins[bin[k]], 1);
+  __syncthreads();
+  if (tid < kWave) {
+    const int cnt = tid < kBins ? s_bins[tid] : 0;
+    const int inc = wave_inclusive_scan(cnt, tid);
+    if (tid < kBins) s_bins[tid] = inc - cnt;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (b0 + k < batch) {
+      const int pos = atomicAdd(&s_bins[bin[k]], 1);
+      s_order[pos] = b0 + k;
+      s_prefix[pos] = nparts[k];
+    }
+  }
+  __syncthreads();
+  // Thread t now owns work positions [t * kPer, t * kPer + kPer): counts -> prefixes.
   int run = 0;
-  for (int bi = b0; bi < b1; ++bi) run += parts_of(bi);
-  s_scan[tid] = run;
-  __syncthreads();
-  for (int off = 1; off < kDecodeThreads; off <<= 1) {
-    const int v = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    nparts[k] = b0 + k < batch ? s_prefix[b0 + k] : 0;
+    run += nparts[k];
   }
-  run = tid > 0 ? s_scan[tid - 1] : 0;
-  for (int bi = b0; bi < b1; ++bi) {
-    s_prefix[bi] = run;
-    run += parts_of(bi);
+  int seq_items = 0;
+  int base = block_exclusive_scan(run, s_wave, seq_items);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (b0 + k < batch) s_prefix[b0 + k] = base;
+    base += nparts[k];
   }
-  if (tid == 0) s_prefix[batch] = s_scan[kDecodeThreads - 1];
+  if (tid == 0) s_prefix[batch] = seq_items;
   __syncthreads();
-  const int total = s_prefix[batch] * p.num_kv_heads;
+  const int total = seq_items * p.num_kv_heads;
 
   // ---- item loop ------------------------------------------------------------------------
   for (int it = 0;; ++it) {
@@ -826,16 +889,16 @@ __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel
     // Ask for the next ticket now; its value is only needed at the end of this
     // item, so the request's latency hides behind the item's loads.
     int next = 0;
-    if (tid == 0) next = atomicAdd(&counters[0], 1);
+    if (tid == 0) next = (int)gridDim.x + atomicAdd(&counters[0], 1);
     const int sp = item / p.num_kv_heads;
     const int hk = item - sp * p.num_kv_heads;
-    int lo = 0, hi = batch;  // largest b with s_prefix[b] <= sp
+    int lo = 0, hi = batch;  // largest work position with s_prefix[pos] <= sp
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (s_prefix[mid] <= sp) lo = mid; else hi = mid;
     }
-    const int b = lo;
-    const int part = sp - s_prefix[b];
+    const int b = s_order[lo];
+    const int part = sp - s_prefix[lo];
     int64_t c = p.context_lens[b];
     c = c < 0 ? 0 : (c > cap ? cap : c);
     const int ctx = (int)c;
