@@ -364,11 +364,14 @@ NIA_DEVICE float wave_sum(float x) {
 }
 
 // Merge the partition partials of (sequence, head) pairs: one wave per pair, each
-// lane owning D / 64 output dims.  Lane i first holds partition i's (m, l) (64 at a
-// time), so the global max and the weights exp2(m_i - M) take one load and two wave
-// reductions; the partial outputs are then accumulated eight partitions per round of
-// independent loads.  Pairs whose sequence has at most one partition were finished
-// by the partial kernel.
+// lane owning D / 64 output dims.  The loads that do not depend on each other go
+// out together: lane i's (m, l) of partition i (64 at a time) and the partial
+// output rows of the first kCombinePrefetch partitions; the global max and the
+// weights exp2(m_i - M) then take two wave reductions, and any further partitions
+// are accumulated eight per round of loads.  Pairs whose sequence has at most one
+// partition were finished by the partial kernel.
+constexpr int kCombinePrefetch = 16;
+
 template <typename T, int D, int BS, int PART_BLOCKS>
 __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine_kernel(DecodeParams p,
                                                                                int batch) {
@@ -389,32 +392,48 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine_kernel(D
   if (nparts <= 1) return;
   const int64_t slot0 = ((int64_t)b * p.num_heads + h) * p.max_parts;
   const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + slot0;
-  float mt = -INFINITY;
-  for (int c0 = 0; c0 < nparts; c0 += kWave)
+  const float* po = p.ws_o + slot0 * D + DL * lane;
+
+  const float2 ml0 = lane < nparts ? ml[lane] : make_float2(-INFINITY, 0.f);
+  float2 o[kCombinePrefetch];
+#pragma unroll
+  for (int j = 0; j < kCombinePrefetch; ++j)
+    o[j] = j < nparts ? *reinterpret_cast<const float2*>(po + (int64_t)j * D)
+                      : make_float2(0.f, 0.f);
+  float mt = ml0.x;
+  for (int c0 = kWave; c0 < nparts; c0 += kWave)
     if (c0 + lane < nparts) mt = fmaxf(mt, ml[c0 + lane].x);
   mt = wave_max(mt);
+
   float lt = 0.f;
   float2 acc = make_float2(0.f, 0.f);
-  const float* po = p.ws_o + slot0 * D + DL * lane;
   for (int c0 = 0; c0 < nparts; c0 += kWave) {
-    float w = 0.f;
-    if (c0 + lane < nparts) {
-      const float2 v = ml[c0 + lane];
-      w = v.x == -INFINITY ? 0.f : fast_exp2(v.x - mt);
-      lt = fmaf(v.y, w, lt);
-    }
+    const float2 v = c0 == 0 ? ml0 : (c0 + lane < nparts ? ml[c0 + lane]
+                                                          : make_float2(-INFINITY, 0.f));
+    const float w = v.x == -INFINITY ? 0.f : fast_exp2(v.x - mt);
+    lt = fmaf(v.y, w, lt);
     const int cnt = min(kWave, nparts - c0);
-    for (int j0 = 0; j0 < cnt; j0 += 8) {
-      float2 o[8];
+    int j0 = 0;
+    if (c0 == 0) {
+#pragma unroll
+      for (int j = 0; j < kCombinePrefetch; ++j) {
+        const float wj = __shfl(w, j, kWave);
+        acc.x = fmaf(o[j].x, wj, acc.x);
+        acc.y = fmaf(o[j].y, wj, acc.y);
+      }
+      j0 = kCombinePrefetch;
+    }
+    for (; j0 < cnt; j0 += 8) {
+      float2 r[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        o[j] = j0 + j < cnt ? *reinterpret_cast<const float2*>(po + (int64_t)(c0 + j0 + j) * D)
+        r[j] = j0 + j < cnt ? *reinterpret_cast<const float2*>(po + (int64_t)(c0 + j0 + j) * D)
                             : make_float2(0.f, 0.f);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float wj = __shfl(w, j0 + j, kWave);
-        acc.x = fmaf(o[j].x, wj, acc.x);
-        acc.y = fmaf(o[j].y, wj, acc.y);
+        const float wj = __shfl(w, (j0 + j) & (kWave - 1), kWave);
+        acc.x = fmaf(r[j].x, wj, acc.x);
+        acc.y = fmaf(r[j].y, wj, acc.y);
       }
     }
   }
@@ -797,27 +816,20 @@ NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
 }
 
 // Persistent variant: a grid of as many workgroups as the chip holds at once.
-// Work items are (sequence, partition, KV head), numbered on the device from
-// context_lens; workgroup w starts with item w and then takes items from an
-// atomic ticket counter (the next ticket is requested while the current item
-// runs), so the grid never carries empty workgroups and a short item is
-// followed at once by the next.
-// Sequences enter the queue in decreasing order of their item size (blocks per
-// partition), so the last tickets are the shortest items and the workgroups
-// finish close together.  Partials go to paged_decode_combine_kernel, launched
-// after this one.  The two counters live at the start of the workspace: they
-// must be zero before the first call, and the last workgroup to leave returns
-// them to zero.
+// Work items are (sequence, partition, KV head) in that order, numbered on the
+// device from context_lens; workgroup w starts with item w and then takes items
+// from an atomic ticket counter (the next ticket is requested while the current
+// item runs), so the grid never carries empty workgroups and a short item is
+// followed at once by the next.  Partials go to paged_decode_combine_kernel,
+// launched after this one.  The two counters live at the start of the
+// workspace: they must be zero before the first call, and the last workgroup to
+// leave returns them to zero.
 template <int G, int PART_BLOCKS>
 __global__ __launch_bounds__(kDecodeThreads)
 __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
-  constexpr int kBins = PART_BLOCKS + 1;  // item sizes 0 (no keys) .. PART_BLOCKS
-  static_assert(kBins <= kWave, "one wave scans the size bins");
-  __shared__ int s_prefix[kPersistentMaxBatch + 1];  // work order: first item of each sequence
-  __shared__ int s_order[kPersistentMaxBatch];       // work order -> sequence
-  __shared__ int s_bins[kBins];
+  __shared__ int s_prefix[kPersistentMaxBatch + 1];  // first item number of each sequence
   __shared__ int s_wave[kDecodeWaves];
   __shared__ int s_ticket[2];
   const int tid = threadIdx.x;
@@ -825,50 +837,24 @@ __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel
 
   // The first item is the workgroup's own id; later tickets come from the counter,
   // offset by the grid size.  (All workgroups asking one counter at launch would
-  // queue on it for about 10 us before any KV load.)
+  // queue on it for several microseconds before any KV load.)
   if (tid == 0) s_ticket[0] = blockIdx.x;
 
   // ---- work index -------------------------------------------------------------------------
-  // Thread t owns sequences [t * kPer, t * kPer + kPer); their context lengths are
-  // loaded together, once.  A counting sort over the item size (bins in LDS) gives
-  // the work order, then a workgroup scan the first item number of each sequence.
+  // Thread t owns sequences [t * kPer, t * kPer + kPer): their context lengths are
+  // loaded together, once, and a workgroup scan of the partition counts gives each
+  // sequence's first item number.
   constexpr int kPer = (kPersistentMaxBatch + kDecodeThreads - 1) / kDecodeThreads;
   const int b0 = tid * kPer;
-  int nparts[kPer], bin[kPer];
+  int nparts[kPer];
+  int run = 0;
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     int64_t c = b0 + k < batch ? p.context_lens[b0 + k] : 0;
     c = c < 0 ? 0 : (c > cap ? cap : c);
     const int blocks = (int)((c + BS - 1) / BS);
-    nparts[k] = blocks > 0 ? (blocks + PART_BLOCKS - 1) / PART_BLOCKS : 1;  // 1 zero-fill item
-    bin[k] = PART_BLOCKS - (blocks + nparts[k] - 1) / nparts[k];  // bin 0 = largest items
-  }
-  if (tid < kBins) s_bins[tid] = 0;
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kPer; ++k)
-    if (b0 + k < batch) atomicAdd(&s_bins[bin[k]], 1);
-  __syncthreads();
-  if (tid < kWave) {
-    const int cnt = tid < kBins ? s_bins[tid] : 0;
-    const int inc = wave_inclusive_scan(cnt, tid);
-    if (tid < kBins) s_bins[tid] = inc - cnt;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    if (b0 + k < batch) {
-      const int pos = atomicAdd(&s_bins[bin[k]], 1);
-      s_order[pos] = b0 + k;
-      s_prefix[pos] = nparts[k];
-    }
-  }
-  __syncthreads();
-  // Thread t now owns work positions [t * kPer, t * kPer + kPer): counts -> prefixes.
-  int run = 0;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    nparts[k] = b0 + k < batch ? s_prefix[b0 + k] : 0;
+    // a sequence without keys is one item (it writes the zero output)
+    nparts[k] = b0 + k < batch ? (blocks > 0 ? (blocks + PART_BLOCKS - 1) / PART_BLOCKS : 1) : 0;
     run += nparts[k];
   }
   int seq_items = 0;
@@ -892,13 +878,13 @@ __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel
     if (tid == 0) next = (int)gridDim.x + atomicAdd(&counters[0], 1);
     const int sp = item / p.num_kv_heads;
     const int hk = item - sp * p.num_kv_heads;
-    int lo = 0, hi = batch;  // largest work position with s_prefix[pos] <= sp
+    int lo = 0, hi = batch;  // largest b with s_prefix[b] <= sp
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (s_prefix[mid] <= sp) lo = mid; else hi = mid;
     }
-    const int b = s_order[lo];
-    const int part = sp - s_prefix[lo];
+    const int b = lo;
+    const int part = sp - s_prefix[b];
     int64_t c = p.context_lens[b];
     c = c < 0 ? 0 : (c > cap ? cap : c);
     const int ctx = (int)c;
