@@ -223,6 +223,26 @@ def bench_decode_vl(torch, ops, workloads):
                 bytes=c.decode_bytes())
 
 
+def bench_decode_fp8(torch, ops, workloads, c):
+    """Paged decode over the fp8 format of the same Qwen3-8B pool (e4m3 codes plus one
+    fp32 scale per row, written by the fp8 KV-write kernel); GB/s of the fp8 bytes."""
+    f8 = workloads.quantize_cache_fp8(c)
+    out = torch.empty_like(c.q)
+
+    def decode(i):
+        L = i % DECODE_LAYERS
+        ops.paged_decode(c.q, f8.k_cache[L], f8.v_cache[L], c.block_tables, c.context_lens,
+                         out=out, k_scale=f8.k_scale[L], v_scale=f8.v_scale[L])
+
+    warm_up(torch, decode)
+    ms = per_call_ms(torch, decode, 40)
+    byts = workloads.fp8_decode_bytes(c)
+    gbps = byts / (ms * 1e-3) / 1e9
+    del f8
+    return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
+                bytes=byts, format="e4m3 codes + fp32 scale per (token, KV head) row")
+
+
 def bench_e2e(torch, mixed: bool):
     """Whole-model generation on the Qwen3-0.6B architecture (random-initialised bf16):
     64 prompts of U[128, 2048] random ids, 256 greedy tokens each.  ``mixed``:
@@ -346,6 +366,7 @@ def main() -> int:
     value = step_bytes / (ms_step * 1e-3) / 1e9
     dec_gbps = c.decode_bytes() / (dec_ms * 1e-3) / 1e9
     extra = {"decode_vl": bench_decode_vl(torch, ops, workloads)}
+    extra["decode_qwen3_8b_fp8"] = bench_decode_fp8(torch, ops, workloads, c)
     extra.update(bench_prefill(torch, ops, workloads))
     pf = extra["prefill_qwen3_8b"]
     extra["kv_write_qwen3_8b"] = dict(us=round(wr_ms * 1e3, 2),

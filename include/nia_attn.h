@@ -198,6 +198,86 @@ int32_t nia_qk_norm_rope_kv_write(void* q, int64_t q_tok_stride, int64_t q_head_
                                   void* stream);
 
 /*
+ * fp8 KV-cache format (no counterpart in the reference, whose caches hold the model
+ * dtype, src/nano_inference/kv_cache/allocator.py:35-39): each (token, KV head) row
+ * of head_dim values is stored as OCP float8 e4m3 codes (uint8; 4 exponent bits,
+ * bias 7, max 448, torch.float8_e4m3fn) with one fp32 scale per row in
+ * k_scale / v_scale [num_blocks, num_kv_heads, block_size]:
+ *   scale = max_d |x_d| / 448,  code_d = e4m3(x_d / scale) (round to nearest even),
+ *   x_d ~= code_d * scale;  a zero row stores scale 0 and zero codes.
+ * Half the cache bytes of bf16, so paged decode reads half the bytes.
+ */
+
+/*
+ * KV-cache write into fp8 caches: the loop of src/nano_inference/layers/
+ * attention.py:267-278 with each row quantised as above.  k, v as nia_kv_write
+ * (bf16 or f32 in `dtype`); k_cache, v_cache uint8 [num_blocks, num_kv_heads,
+ * block_size, 128]; slots < 0 or >= num_blocks * block_size are skipped.
+ * Supported: head_dim 128.
+ */
+int32_t nia_kv_write_fp8(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                         const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                         void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+                         const int64_t* slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t dtype,
+                         void* stream);
+
+/*
+ * nia_qk_norm_rope_kv_write with fp8 caches: q and k are normalised and rotated in
+ * place exactly as there, and the rotated k row and the v row are written to the
+ * caches in the fp8 format above (k_cache, v_cache uint8; k_scale, v_scale fp32).
+ */
+int32_t nia_qk_norm_rope_kv_write_fp8(void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                      void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                      const void* v, int64_t v_tok_stride,
+                                      int64_t v_head_stride, const void* q_norm_weight,
+                                      const void* k_norm_weight, float eps,
+                                      const int64_t* positions, int64_t pos_axis_stride,
+                                      int32_t num_axes, const float* inv_freq,
+                                      int32_t mrope_section0, int32_t mrope_section1,
+                                      void* k_cache, void* v_cache, float* k_scale,
+                                      float* v_scale, const int64_t* slot_mapping,
+                                      int32_t num_tokens, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t block_size, int64_t num_blocks, int32_t dtype,
+                                      void* stream);
+
+/*
+ * Paged decode over fp8 caches: nia_paged_decode with k_cache / v_cache in the fp8
+ * format above (uint8 codes, k_scale / v_scale fp32 [num_blocks, num_kv_heads,
+ * block_size]).  q and out are bf16; keys are dequantised exactly as
+ * code * row scale (the code is widened to bf16 without rounding, the scale
+ * multiplies the q . k score, and each softmax weight carries its row's v scale).
+ * Same workspace contract and shapes as nia_paged_decode (head_dim 128, block
+ * size 16, num_heads / num_kv_heads <= 8).
+ */
+int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride, int64_t out_head_stride,
+                             const void* q, int64_t q_batch_stride, int64_t q_head_stride,
+                             const void* k_cache, const void* v_cache, const float* k_scale,
+                             const float* v_scale, const int32_t* block_tables,
+                             int32_t bt_stride, int32_t max_blocks_per_seq,
+                             const int64_t* context_lens, int32_t batch, int32_t num_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                             int64_t num_blocks, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
+ * fp8 cache -> contiguous bf16 rows, for chunked prefill over an fp8 cache: the keys
+ * [0, context_lens[s]) of sequence s, gathered through its block table as
+ * nia_paged_decode reads them and dequantised (code * row scale, rounded to bf16),
+ * land in rows s * seq_stride + t of out_k / out_v [batch * seq_stride][num_kv_heads]
+ * [128] (seq_stride >= max_blocks_per_seq * block_size; rows past a context are not
+ * written).  nia_prefill over those rows with k_start[s] = s * seq_stride and
+ * NIA_CAUSAL_BOTTOM_RIGHT then gives nia_prefill_paged's result.
+ */
+int32_t nia_dequant_gather_fp8(const void* k_cache, const void* v_cache, const float* k_scale,
+                               const float* v_scale, const int32_t* block_tables,
+                               int32_t bt_stride, int32_t max_blocks_per_seq,
+                               const int64_t* context_lens, int32_t batch, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                               void* out_k, void* out_v, int64_t seq_stride, void* stream);
+
+/*
  * Step metadata: the padded model inputs and attention metadata of one engine
  * step, expanded on the device from a compact descriptor (one upload per step).
  * Replaces the loops of src/nano_inference/engine/context_builder.py:83-193

@@ -47,6 +47,11 @@ SIGNATURES = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p,
          _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _sz, _i32, _p],
     ),
+    "nia_paged_decode_fp8": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i32, _p,
+         _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _sz, _p],
+    ),
     "nia_prefill": (
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64,
@@ -61,6 +66,20 @@ SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _p, _i64, _i32,
          _p, _i32, _i32, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p],
+    ),
+    "nia_kv_write_fp8": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64,
+         _i32, _p],
+    ),
+    "nia_qk_norm_rope_kv_write_fp8": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _p, _i64, _i32,
+         _p, _i32, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i64, _i32, _p],
+    ),
+    "nia_dequant_gather_fp8": (
+        _i32,
+        [_p, _p, _p, _p, _p, _i32, _i32, _p, _i32, _i32, _i32, _i32, _i64, _p, _p, _i64, _p],
     ),
     "nia_step_metadata": (
         _i32,

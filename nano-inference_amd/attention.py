@@ -150,6 +150,12 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         """(positions, mrope_section) for the fused kernel: 1-D RoPE here."""
         return position_ids, None
 
+    def _scales(self, metadata):
+        """This layer's fp8 row scales (None for caches in the model dtype)."""
+        if metadata is None or metadata.k_scale is None or metadata.v_scale is None:
+            return None, None
+        return metadata.k_scale[self.layer_idx], metadata.v_scale[self.layer_idx]
+
     def _qkv(self, x, position_ids, metadata, k_cache=None, v_cache=None):
         """Projected, normalised and rotated q, k and v; the last item tells whether
         k/v were also written to (k_cache, v_cache) through the metadata's slots."""
@@ -163,12 +169,13 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
             write = k_cache is not None and metadata is not None and \
                 metadata.slot_mapping is not None
             norm = self.q_norm is not None
+            ks, vs = self._scales(metadata) if write else (None, None)
             ops.qk_norm_rope_kv_write(
                 q, k, v, self.q_norm.weight if norm else None,
                 self.k_norm.weight if norm else None, self.q_norm.eps if norm else 0.0,
                 pos, self.rotary.inv_freq, section,
                 k_cache if write else None, v_cache if write else None,
-                metadata.slot_mapping if write else None)
+                metadata.slot_mapping if write else None, ks, vs)
             return q, k, v, write
         if self.q_norm is not None:
             q = self.q_norm(q)
@@ -213,11 +220,12 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
 
         # 1. KV write (src/nano_inference/layers/attention.py:267-278), unless the
         # fused QK kernel already wrote the step's rows.
+        ks, vs = self._scales(metadata)
         if not written and k_cache is not None and metadata.slot_mapping is not None:
-            ops.kv_write(k, v, k_cache, v_cache, metadata.slot_mapping)
+            ops.kv_write(k, v, k_cache, v_cache, metadata.slot_mapping, ks, vs)
 
         if isinstance(metadata, PackedAttentionMetadata):
-            attn = self._packed_attention(q, k_cache, v_cache, metadata)
+            attn = self._packed_attention(q, k_cache, v_cache, metadata, ks, vs)
         elif metadata.is_prefill:
             # 2a. Prefill attends over the step's fresh K/V (:281-284).  Padded
             # rows past a sequence's length see all its keys, as in the reference.
@@ -228,7 +236,8 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
             ctx = metadata.context_lens
             if s == 1:
                 # 2b. Decode: gather + GQA + mask + softmax in one kernel (:285-332).
-                attn = ops.paged_decode(q[:, 0], k_cache, v_cache, bt, ctx)
+                attn = ops.paged_decode(q[:, 0], k_cache, v_cache, bt, ctx, k_scale=ks,
+                                        v_scale=vs)
             else:
                 # 2c. Several new tokens on top of cached context: chunked prefill.
                 dev = x.device
@@ -238,13 +247,14 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
                                    device=dev)
                 ops.prefill_paged(q.reshape(b * s, self.num_heads, self.head_dim), k_cache,
                                   v_cache, bt, q_start, q_len, ctx, s,
-                                  ops.CAUSAL_BOTTOM_RIGHT, out=attn)
+                                  ops.CAUSAL_BOTTOM_RIGHT, out=attn, k_scale=ks, v_scale=vs)
         else:
             attn = self._dense_causal(q, k, v, attention_mask)
         return self.o_proj(attn.reshape(b, s, self.num_heads * self.head_dim))
 
 
-    def _packed_attention(self, q, k_cache, v_cache, md: PackedAttentionMetadata):
+    def _packed_attention(self, q, k_cache, v_cache, md: PackedAttentionMetadata, ks=None,
+                          vs=None):
         """Decode rows through the decode kernel, chunk rows through the chunked
         prefill kernel, both reading the paged cache the step has just written."""
         if k_cache is None:
@@ -256,11 +266,11 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         n = md.q_start.shape[0]
         if nd > 0:
             ops.paged_decode(q2[:nd], k_cache, v_cache, md.kv_block_tables[:nd],
-                             md.context_lens[:nd], out=out[:nd])
+                             md.context_lens[:nd], out=out[:nd], k_scale=ks, v_scale=vs)
         if nd < n:
             ops.prefill_paged(q2, k_cache, v_cache, md.kv_block_tables[nd:], md.q_start[nd:],
                               md.q_len[nd:], md.context_lens[nd:], md.max_q_len,
-                              ops.CAUSAL_BOTTOM_RIGHT, out=out)
+                              ops.CAUSAL_BOTTOM_RIGHT, out=out, k_scale=ks, v_scale=vs)
         return out
 
 

@@ -16,7 +16,8 @@ import torch
 
 @dataclass
 class AttentionMetadata:
-    """Metadata required for paged attention (same fields as the reference)."""
+    """Metadata required for paged attention: the reference's fields in its order,
+    plus the optional row scales of fp8 caches (default None)."""
 
     context_lens: torch.Tensor  # (B,) int64 - total sequence length per request
     kv_block_tables: torch.Tensor  # (B, max_blocks_per_seq) int32, zero-padded
@@ -31,6 +32,11 @@ class AttentionMetadata:
 
     # VLM only: (3, B, S_step) mRoPE position ids; None for text-only batches.
     mrope_position_ids: Optional[torch.Tensor] = None
+
+    # fp8 caches only (not in the reference): per-row scales [L, num_blocks, H_kv,
+    # block_size] float32 beside uint8 / float8_e4m3fn k_cache / v_cache.
+    k_scale: Optional[torch.Tensor] = None
+    v_scale: Optional[torch.Tensor] = None
 
 
 @dataclass

@@ -46,6 +46,21 @@ NIA_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
 
 NIA_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- fp8 (OCP e4m3: 4 exponent bits, bias 7, 3 mantissa bits, max 448) ----------
+
+constexpr float kE4m3Max = 448.f;
+
+// Two floats -> two e4m3 codes in the low 16 bits, round to nearest even.
+NIA_DEVICE uint32_t fp8x2_from_f32(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+
+// Two e4m3 codes (bytes 2 * HI, 2 * HI + 1 of `w`) -> bf16 pair, exact.
+template <bool HI>
+NIA_DEVICE uint32_t bf16x2_from_fp8x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
+}
+
 // ---- cross-lane -------------------------------------------------------------
 
 // DPP controls (GCN/CDNA encoding).

@@ -53,6 +53,16 @@ constexpr float kLazyRescale = 8.0f;
 // during P V (32 more VGPRs than the plain loop).
 constexpr int kRollingMaxG = 4;
 
+// Workgroups per CU of the persistent kernel.  Two (8 waves, a 256-VGPR budget)
+// for bf16 caches and large groups; fp8 caches with G <= 4 run the plain loop at
+// three (12 waves): a pair of fp8 block-heads is half the bytes, so more waves
+// keep enough loads in flight (measured 152 -> 142 us on the Qwen3-8B workload;
+// the rolling loop does not fit three waves' registers).
+constexpr int persistent_waves(int G, bool fp8) { return fp8 && G <= kRollingMaxG ? 3 : 2; }
+constexpr bool rolling_loop(int G, bool fp8) {
+  return G <= kRollingMaxG && persistent_waves(G, fp8) == 2;
+}
+
 struct DecodeParams {
   void* out;
   int64_t out_b, out_h;
@@ -60,6 +70,8 @@ struct DecodeParams {
   int64_t q_b, q_h;
   const void* k_cache;
   const void* v_cache;
+  const float* k_scale;  // fp8 caches: one scale per (block, KV head, slot) row
+  const float* v_scale;
   const int32_t* block_tables;
   int32_t bt_stride;
   int32_t max_blocks;
@@ -444,25 +456,26 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine_kernel(D
   out[1] = E::from_f32(acc.y * inv);
 }
 
-// bf16 decode, head_dim 128, block size 16 (the serving layout).
+// Decode with head_dim 128, block size 16 (the serving layout), bf16 queries, and
+// the cache in bf16 or in the fp8 format (e4m3 codes, one fp32 scale per row).
 //
 // Two lane layouts share one wave:
-//   K layout: 8 lanes per token.  Wave-wide load j of a block reads token
-//     (l / 8) + 8 (j / 2), dims 16 (l % 8) + 8 (j % 2) .. +7, so a q . k dot
-//     product is 8 bf16 dot2 per lane and a 3-step DPP sum over 8 lanes, and
-//     each lane owns 2 tokens per block for the softmax.
+//   K layout: 8 lanes per token; a lane owns 2 tokens per block (l / 8 and
+//     l / 8 + 8) and 16 dims (16 (l % 8) .. +15), so a q . k dot product is 8 bf16
+//     dot2 per lane and a 3-step DPP sum over 8 lanes.  bf16: 4 wave-wide 16-byte
+//     loads per block-head; fp8: 2 (the 16 codes of a lane, converted to bf16 pairs
+//     with v_cvt_scalef32_pk_bf16_fp8, exact) and the row's k scale multiplies the
+//     score.
 //   V layout: 16 lanes per token, fully coalesced: load i reads token 4i + l/16,
-//     dims 8 (l % 16) .. +7.
+//     dims 8 (l % 16) .. +7 (16 bytes in bf16, 8 in fp8).
 // Blocks are processed in pairs (A, B).  For each K-layout token the softmax
 // weights of blocks A and B are packed into one bf16 pair and moved to the
 // V-layout lanes with ds_bpermute; there P.V is v_dot2_f32_bf16 over the
-// (A, B) token pair, with V's two tokens interleaved by v_perm.  The running
-// max is uniform over the wave (raised lazily by more than 2^8), so row and
-// lane partials add without rescaling.  Per 4 KB block-head this is about
-// 64 dot2 (QK) + 64 dot2 (PV) + 24 DPP + ~40 softmax/convert VALU operations.
-// A wave has one pair (16 KB) of loads in flight at a time; latency is hidden
-// across the 4 waves per SIMD that the register budget (<= 128 VGPRs at
-// G <= 4) allows.
+// (A, B) token pair, with V's two tokens interleaved by v_perm (fp8: the codes
+// are interleaved first, then converted, and each weight carries its row's v
+// scale while l sums the unscaled weights).  The running max is uniform over
+// the wave (raised lazily by more than 2^8), so row and lane partials add
+// without rescaling.
 template <int G>
 struct DecodeState {
   uint32_t qw[G][8];
@@ -470,6 +483,17 @@ struct DecodeState {
   float l[G];
   float m[G];
 };
+
+// One block-head in registers: bf16 K (K layout) and V (V layout), fp8 K and V
+// codes plus the row scales of the lane's two K-layout tokens.
+struct KRegs16 { uint4 r[4]; };
+struct VRegs16 { uint4 r[4]; };
+struct KRegs8 { uint4 r[2]; float ks[2]; float vs[2]; };
+struct VRegs8 { uint2 r[4]; };
+
+template <bool FP8> struct KvRegs;
+template <> struct KvRegs<false> { using K = KRegs16; using V = VRegs16; };
+template <> struct KvRegs<true> { using K = KRegs8; using V = VRegs8; };
 
 // Physical block of partition-relative block jx (its table entry sits in lane
 // jx - blk_begin of my_bt), or -1 past the partition or for an invalid id.
@@ -479,61 +503,120 @@ NIA_DEVICE int decode_block_id(const DecodeParams& p, int my_bt, int jx, int blk
   return (blk >= 0 && (int64_t)blk < p.num_blocks) ? blk : -1;
 }
 
-// The 4 wave-wide loads of one block-head's K in the K layout (lane: token
-// lane / 8 and + 8, 16-dim chunk lane % 8); zeros for blk < 0.
-NIA_DEVICE void decode_load_k(const DecodeParams& p, const bf16_t* kcache, int blk, int hk,
-                              int lane, uint4 (&kr)[4]) {
-  constexpr int BS = 16, D = 128;
+// First element of block-head (blk, hk) of a cache with `row_bytes` per row.
+NIA_DEVICE const uint8_t* block_head(const void* cache, const DecodeParams& p, int blk, int hk,
+                                     int row_bytes) {
+  return reinterpret_cast<const uint8_t*>(cache) +
+         ((int64_t)blk * p.num_kv_heads + hk) * 16 * row_bytes;
+}
+
+// K of one block-head in the K layout; zeros for blk < 0.
+NIA_DEVICE void decode_load_k(const DecodeParams& p, int blk, int hk, int lane, KRegs16& kr) {
   const int ktok = lane >> 3, kc = lane & 7;
   if (blk >= 0) {
-    const uint4* kp =
-        reinterpret_cast<const uint4*>(kcache + ((int64_t)blk * p.num_kv_heads + hk) * (BS * D));
-    kr[0] = kp[ktok * 16 + 2 * kc];
-    kr[1] = kp[ktok * 16 + 2 * kc + 1];
-    kr[2] = kp[(ktok + 8) * 16 + 2 * kc];
-    kr[3] = kp[(ktok + 8) * 16 + 2 * kc + 1];
+    const uint4* kp = reinterpret_cast<const uint4*>(block_head(p.k_cache, p, blk, hk, 256));
+    kr.r[0] = kp[ktok * 16 + 2 * kc];
+    kr.r[1] = kp[ktok * 16 + 2 * kc + 1];
+    kr.r[2] = kp[(ktok + 8) * 16 + 2 * kc];
+    kr.r[3] = kp[(ktok + 8) * 16 + 2 * kc + 1];
   } else {
-    kr[0] = kr[1] = kr[2] = kr[3] = make_uint4(0, 0, 0, 0);
+    kr.r[0] = kr.r[1] = kr.r[2] = kr.r[3] = make_uint4(0, 0, 0, 0);
   }
 }
 
-// The 4 wave-wide loads of one block-head's V in the V layout (lane: token
-// 4 i + lane / 16, 8-dim chunk lane % 16); zeros for blk < 0.
-NIA_DEVICE void decode_load_v(const DecodeParams& p, const bf16_t* vcache, int blk, int hk,
-                              int lane, uint4 (&vr)[4]) {
-  constexpr int BS = 16, D = 128;
+NIA_DEVICE void decode_load_k(const DecodeParams& p, int blk, int hk, int lane, KRegs8& kr) {
+  const int ktok = lane >> 3, kc = lane & 7;
   if (blk >= 0) {
-    const uint4* vp =
-        reinterpret_cast<const uint4*>(vcache + ((int64_t)blk * p.num_kv_heads + hk) * (BS * D));
-    vr[0] = vp[lane];
-    vr[1] = vp[64 + lane];
-    vr[2] = vp[128 + lane];
-    vr[3] = vp[192 + lane];
+    const uint8_t* kp = block_head(p.k_cache, p, blk, hk, 128);
+    kr.r[0] = *reinterpret_cast<const uint4*>(kp + ktok * 128 + 16 * kc);
+    kr.r[1] = *reinterpret_cast<const uint4*>(kp + (ktok + 8) * 128 + 16 * kc);
+    const int64_t row0 = ((int64_t)blk * p.num_kv_heads + hk) * 16;
+    kr.ks[0] = p.k_scale[row0 + ktok];
+    kr.ks[1] = p.k_scale[row0 + ktok + 8];
+    kr.vs[0] = p.v_scale[row0 + ktok];
+    kr.vs[1] = p.v_scale[row0 + ktok + 8];
   } else {
-    vr[0] = vr[1] = vr[2] = vr[3] = make_uint4(0, 0, 0, 0);
+    kr.r[0] = kr.r[1] = make_uint4(0, 0, 0, 0);
+    kr.ks[0] = kr.ks[1] = kr.vs[0] = kr.vs[1] = 0.f;
+  }
+}
+
+// V of one block-head in the V layout; zeros for blk < 0.
+NIA_DEVICE void decode_load_v(const DecodeParams& p, int blk, int hk, int lane, VRegs16& vr) {
+  if (blk >= 0) {
+    const uint4* vp = reinterpret_cast<const uint4*>(block_head(p.v_cache, p, blk, hk, 256));
+    vr.r[0] = vp[lane];
+    vr.r[1] = vp[64 + lane];
+    vr.r[2] = vp[128 + lane];
+    vr.r[3] = vp[192 + lane];
+  } else {
+    vr.r[0] = vr.r[1] = vr.r[2] = vr.r[3] = make_uint4(0, 0, 0, 0);
+  }
+}
+
+NIA_DEVICE void decode_load_v(const DecodeParams& p, int blk, int hk, int lane, VRegs8& vr) {
+  if (blk >= 0) {
+    const uint2* vp = reinterpret_cast<const uint2*>(block_head(p.v_cache, p, blk, hk, 128));
+    vr.r[0] = vp[lane];
+    vr.r[1] = vp[64 + lane];
+    vr.r[2] = vp[128 + lane];
+    vr.r[3] = vp[192 + lane];
+  } else {
+    vr.r[0] = vr.r[1] = vr.r[2] = vr.r[3] = make_uint2(0, 0);
   }
 }
 
 // Zero the V rows of one 16-token block (V layout) that lie past the context
-// or belong to an invalid block id.
-NIA_DEVICE void zero_invalid_v(uint4 (&v)[4], bool ok, int tok0, int ctx, int vrow) {
+// or belong to an invalid block id: stale slots may hold any bits (NaN codes
+// included), and 0 * NaN would poison the sums.
+template <typename VRegs>
+NIA_DEVICE void zero_invalid_v(VRegs& v, bool ok, int tok0, int ctx, int vrow) {
   if (ok && tok0 + 16 <= ctx) return;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const bool valid = ok && (tok0 + 4 * i + vrow) < ctx;
-    v[i].x = valid ? v[i].x : 0u;
-    v[i].y = valid ? v[i].y : 0u;
-    v[i].z = valid ? v[i].z : 0u;
-    v[i].w = valid ? v[i].w : 0u;
+    if constexpr (std::is_same<VRegs, VRegs16>::value) {
+      v.r[i].x = valid ? v.r[i].x : 0u;
+      v.r[i].y = valid ? v.r[i].y : 0u;
+      v.r[i].z = valid ? v.r[i].z : 0u;
+      v.r[i].w = valid ? v.r[i].w : 0u;
+    } else {
+      v.r[i].x = valid ? v.r[i].x : 0u;
+      v.r[i].y = valid ? v.r[i].y : 0u;
+    }
   }
 }
 
+// The 8 bf16 pairs of one K-layout token (16 dims) and its score multiplier.
+NIA_DEVICE void k_token_pairs(const KRegs16& k, int sl, uint32_t (&w)[8]) {
+  const uint4 a = k.r[2 * sl], b = k.r[2 * sl + 1];
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+NIA_DEVICE void k_token_pairs(const KRegs8& k, int sl, uint32_t (&w)[8]) {
+  const uint4 a = k.r[sl];
+  w[0] = bf16x2_from_fp8x2<false>(a.x);
+  w[1] = bf16x2_from_fp8x2<true>(a.x);
+  w[2] = bf16x2_from_fp8x2<false>(a.y);
+  w[3] = bf16x2_from_fp8x2<true>(a.y);
+  w[4] = bf16x2_from_fp8x2<false>(a.z);
+  w[5] = bf16x2_from_fp8x2<true>(a.z);
+  w[6] = bf16x2_from_fp8x2<false>(a.w);
+  w[7] = bf16x2_from_fp8x2<true>(a.w);
+}
+
+NIA_DEVICE float k_token_scale(const KRegs16&, int) { return 1.f; }
+NIA_DEVICE float k_token_scale(const KRegs8& k, int sl) { return k.ks[sl]; }
+NIA_DEVICE float v_token_scale(const KRegs16&, int) { return 1.f; }
+NIA_DEVICE float v_token_scale(const KRegs8& k, int sl) { return k.vs[sl]; }
+
 // Scores of a block pair (K layout), pre-scaled to log2 units; -inf past the
 // context or in an invalid block.
-template <int G>
-NIA_DEVICE void decode_qk_pair(const DecodeParams& p, const DecodeState<G>& st,
-                               const uint4 (&kA)[4], const uint4 (&kB)[4], bool okA, bool okB,
-                               int jb, int ctx, int lane, float (&xs)[2][2][G]) {
+template <int G, typename KRegs>
+NIA_DEVICE void decode_qk_pair(const DecodeParams& p, const DecodeState<G>& st, const KRegs& kA,
+                               const KRegs& kB, bool okA, bool okB, int jb, int ctx, int lane,
+                               float (&xs)[2][2][G]) {
   constexpr int BS = 16;
   const int ktok = lane >> 3;
 #pragma unroll
@@ -541,32 +624,70 @@ NIA_DEVICE void decode_qk_pair(const DecodeParams& p, const DecodeState<G>& st,
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
       const bool valid = (x ? okB : okA) && ((jb + x) * BS + 8 * sl + ktok) < ctx;
-      const uint4 k0 = x ? kB[2 * sl] : kA[2 * sl];
-      const uint4 k1 = x ? kB[2 * sl + 1] : kA[2 * sl + 1];
+      uint32_t w[8];
+      k_token_pairs(x ? kB : kA, sl, w);
+      const float mult = k_token_scale(x ? kB : kA, sl) * p.scale_log2;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        float s = dot2_bf16(st.qw[g][0], k0.x, 0.f);
-        s = dot2_bf16(st.qw[g][1], k0.y, s);
-        s = dot2_bf16(st.qw[g][2], k0.z, s);
-        s = dot2_bf16(st.qw[g][3], k0.w, s);
-        s = dot2_bf16(st.qw[g][4], k1.x, s);
-        s = dot2_bf16(st.qw[g][5], k1.y, s);
-        s = dot2_bf16(st.qw[g][6], k1.z, s);
-        s = dot2_bf16(st.qw[g][7], k1.w, s);
+        float s = dot2_bf16(st.qw[g][0], w[0], 0.f);
+#pragma unroll
+        for (int e = 1; e < 8; ++e) s = dot2_bf16(st.qw[g][e], w[e], s);
         s = group_sum<8>(s);
-        xs[x][sl][g] = valid ? s * p.scale_log2 : -INFINITY;
+        xs[x][sl][g] = valid ? s * mult : -INFINITY;
       }
     }
   }
 }
 
-// Online-softmax update and O += P V for a block pair (V layout).
+// O += P V over one V-layout load i (4 tokens of blocks A and B): pv[g] holds the
+// lane's token weights (A, B) as a bf16 pair.
 template <int G>
+NIA_DEVICE void pv_accumulate(DecodeState<G>& st, const uint32_t (&pv)[G], const VRegs16& vA,
+                              const VRegs16& vB, int i) {
+  const uint32_t va[4] = {vA.r[i].x, vA.r[i].y, vA.r[i].z, vA.r[i].w};
+  const uint32_t vb[4] = {vB.r[i].x, vB.r[i].y, vB.r[i].z, vB.r[i].w};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);
+    const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      st.o[g][2 * w] = dot2_bf16(pv[g], lo, st.o[g][2 * w]);
+      st.o[g][2 * w + 1] = dot2_bf16(pv[g], hi, st.o[g][2 * w + 1]);
+    }
+  }
+}
+
+template <int G>
+NIA_DEVICE void pv_accumulate(DecodeState<G>& st, const uint32_t (&pv)[G], const VRegs8& vA,
+                              const VRegs8& vB, int i) {
+  const uint32_t va[2] = {vA.r[i].x, vA.r[i].y};
+  const uint32_t vb[2] = {vB.r[i].x, vB.r[i].y};
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    // codes (a0 b0 a1 b1) and (a2 b2 a3 b3), then (A, B) bf16 pairs per dim
+    const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07030602u);
+    const uint32_t d[4] = {bf16x2_from_fp8x2<false>(lo), bf16x2_from_fp8x2<true>(lo),
+                           bf16x2_from_fp8x2<false>(hi), bf16x2_from_fp8x2<true>(hi)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < G; ++g) st.o[g][4 * w + j] = dot2_bf16(pv[g], d[j], st.o[g][4 * w + j]);
+  }
+}
+
+// Online-softmax update and O += P V for a block pair (V layout).  kA, kB supply
+// the fp8 rows' v scales (K layout); the weights that multiply V carry them.
+template <int G, typename KRegs, typename VRegs>
 NIA_DEVICE void decode_pv_pair(const DecodeParams& p, DecodeState<G>& st,
-                               const float (&xs)[2][2][G], uint4 (&vA)[4], uint4 (&vB)[4],
-                               bool okA, bool okB, int jb, int ctx, int lane) {
+                               const float (&xs)[2][2][G], const KRegs& kA, const KRegs& kB,
+                               VRegs& vA, VRegs& vB, bool okA, bool okB, int jb, int ctx,
+                               int lane) {
   constexpr int BS = 16;
+  constexpr bool kScaled = std::is_same<KRegs, KRegs8>::value;
   const int vrow = lane >> 4;
+  const int ktok = lane >> 3;
   // ---- lazy wave-uniform running max -------------------------------------------------------
   float bm[G];
   bool need = false;
@@ -587,6 +708,17 @@ NIA_DEVICE void decode_pv_pair(const DecodeParams& p, DecodeState<G>& st,
     }
   }
   // ---- weights, packed (A, B) per token ----------------------------------------------------
+  float vsa[2], vsb[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    if constexpr (kScaled) {
+      // a stale row's scale may be any value: weights past the context are 0 * 0
+      vsa[sl] = okA && (jb * BS + 8 * sl + ktok) < ctx ? v_token_scale(kA, sl) : 0.f;
+      vsb[sl] = okB && ((jb + 1) * BS + 8 * sl + ktok) < ctx ? v_token_scale(kB, sl) : 0.f;
+    } else {
+      vsa[sl] = vsb[sl] = 1.f;
+    }
+  }
   uint32_t pp[2][G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -596,11 +728,9 @@ NIA_DEVICE void decode_pv_pair(const DecodeParams& p, DecodeState<G>& st,
       const float pa = fast_exp2(xs[0][sl][g] - msub);
       const float pb2 = fast_exp2(xs[1][sl][g] - msub);
       st.l[g] += pa + pb2;
-      pp[sl][g] = pack_bf16x2(pa, pb2);
+      pp[sl][g] = kScaled ? pack_bf16x2(pa * vsa[sl], pb2 * vsb[sl]) : pack_bf16x2(pa, pb2);
     }
   }
-  // Slots past the context (or in an invalid block) hold stale data of any
-  // value: zero their V so that 0 * garbage cannot produce NaN.
   zero_invalid_v(vA, okA, jb * BS, ctx, vrow);
   zero_invalid_v(vB, okB, (jb + 1) * BS, ctx, vrow);
   // ---- O += P V (V layout) -----------------------------------------------------------------
@@ -615,18 +745,7 @@ NIA_DEVICE void decode_pv_pair(const DecodeParams& p, DecodeState<G>& st,
     for (int g = 0; g < G; ++g)
       pv[g] = (uint32_t)__builtin_amdgcn_ds_bpermute((i & 1) ? bp_addr1 : bp_addr0,
                                                      (int)pp[i >> 1][g]);
-    const uint32_t va[4] = {vA[i].x, vA[i].y, vA[i].z, vA[i].w};
-    const uint32_t vb[4] = {vB[i].x, vB[i].y, vB[i].z, vB[i].w};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);
-      const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        st.o[g][2 * w] = dot2_bf16(pv[g], lo, st.o[g][2 * w]);
-        st.o[g][2 * w + 1] = dot2_bf16(pv[g], hi, st.o[g][2 * w + 1]);
-      }
-    }
+    pv_accumulate<G>(st, pv, vA, vB, i);
   }
 }
 
@@ -639,23 +758,23 @@ NIA_DEVICE void decode_partition(int ctx_blocks, int part_blocks, int part, int&
   end = (int)(((int64_t)(part + 1) * ctx_blocks) / nparts);
 }
 
-// One work item of the bf16 decode: partition `part` (blocks [blk_begin,
-// blk_end)) of sequence b and KV head hk, all G query heads of the group.  The
-// workgroup's 4 waves take the partition's block pairs round-robin; their
-// states merge through LDS and leave as the final output (single-partition
-// sequence) or as a partial for the partition merge.
-template <int G, int PART_BLOCKS>
-NIA_DEVICE void decode_bf16_item(const DecodeParams& p, int b, int hk, int part, int nparts,
-                                 int blk_begin, int blk_end, int ctx) {
+// One work item: partition `part` (blocks [blk_begin, blk_end)) of sequence b and
+// KV head hk, all G query heads of the group, over a bf16 or an fp8 cache.  The
+// workgroup's 4 waves take the partition's block pairs round-robin; their states
+// merge through LDS and leave as the final output (single-partition sequence) or
+// as a partial for the partition merge.
+template <int G, int PART_BLOCKS, bool FP8>
+NIA_DEVICE void decode_item(const DecodeParams& p, int b, int hk, int part, int nparts,
+                            int blk_begin, int blk_end, int ctx) {
   constexpr int D = 128;
+  using KR = typename KvRegs<FP8>::K;
+  using VR = typename KvRegs<FP8>::V;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int kc = lane & 7;     // K layout: 16-dim chunk
   const int vrow = lane >> 4;  // V layout: token within a 4-token load
   const int vc = lane & 15;    // V layout: 8-dim chunk
 
-  const bf16_t* kcache = reinterpret_cast<const bf16_t*>(p.k_cache);
-  const bf16_t* vcache = reinterpret_cast<const bf16_t*>(p.v_cache);
   const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
 
   // The partition's block-table slice, one entry per lane, read once so that
@@ -681,39 +800,42 @@ NIA_DEVICE void decode_bf16_item(const DecodeParams& p, int b, int hk, int part,
 
   {
     constexpr int kStep = 2 * kDecodeWaves;
-    if constexpr (G <= kRollingMaxG) {
+    if constexpr (rolling_loop(G, FP8)) {
       // Rolling pipeline: the next pair's K loads go out as soon as this pair's
       // scores are taken, its V loads as soon as this pair's P V is issued, so a wave
       // keeps loads in flight while it computes.
       int jb = blk_begin + 2 * wave;
       if (jb < blk_end) {
-        uint4 kA[4], vA[4], kB[4], vB[4];
+        KR kA, kB;
+        VR vA, vB;
         int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
         int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
-        decode_load_k(p, kcache, bA, hk, lane, kA);
-        decode_load_v(p, vcache, bA, hk, lane, vA);
-        decode_load_k(p, kcache, bB, hk, lane, kB);
-        decode_load_v(p, vcache, bB, hk, lane, vB);
+        decode_load_k(p, bA, hk, lane, kA);
+        decode_load_v(p, bA, hk, lane, vA);
+        decode_load_k(p, bB, hk, lane, kB);
+        decode_load_v(p, bB, hk, lane, vB);
         for (;;) {
           float xs[2][2][G];
           decode_qk_pair<G>(p, st, kA, kB, bA >= 0, bB >= 0, jb, ctx, lane, xs);
           const int jn = jb + kStep;
           const bool more = jn < blk_end;
           int nA = -1, nB = -1;
+          // fp8: the v scales ride with K; keep this pair's until P V has used them.
+          KR kA2 = kA, kB2 = kB;
           // The next pair's loads reuse this pair's registers: keep them behind the
           // instructions that read those registers.
           __builtin_amdgcn_sched_barrier(0);
           if (more) {
             nA = decode_block_id(p, my_bt, jn, blk_begin, blk_end);
             nB = decode_block_id(p, my_bt, jn + 1, blk_begin, blk_end);
-            decode_load_k(p, kcache, nA, hk, lane, kA);
-            decode_load_k(p, kcache, nB, hk, lane, kB);
+            decode_load_k(p, nA, hk, lane, kA);
+            decode_load_k(p, nB, hk, lane, kB);
           }
-          decode_pv_pair<G>(p, st, xs, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
+          decode_pv_pair<G>(p, st, xs, kA2, kB2, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
           if (!more) break;
           __builtin_amdgcn_sched_barrier(0);
-          decode_load_v(p, vcache, nA, hk, lane, vA);
-          decode_load_v(p, vcache, nB, hk, lane, vB);
+          decode_load_v(p, nA, hk, lane, vA);
+          decode_load_v(p, nB, hk, lane, vB);
           bA = nA;
           bB = nB;
           jb = jn;
@@ -721,16 +843,17 @@ NIA_DEVICE void decode_bf16_item(const DecodeParams& p, int b, int hk, int part,
       }
     } else {
       for (int jb = blk_begin + 2 * wave; jb < blk_end; jb += kStep) {
-        uint4 kA[4], vA[4], kB[4], vB[4];
+        KR kA, kB;
+        VR vA, vB;
         const int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
         const int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
-        decode_load_k(p, kcache, bA, hk, lane, kA);
-        decode_load_v(p, vcache, bA, hk, lane, vA);
-        decode_load_k(p, kcache, bB, hk, lane, kB);
-        decode_load_v(p, vcache, bB, hk, lane, vB);
+        decode_load_k(p, bA, hk, lane, kA);
+        decode_load_v(p, bA, hk, lane, vA);
+        decode_load_k(p, bB, hk, lane, kB);
+        decode_load_v(p, bB, hk, lane, vB);
         float xs[2][2][G];
         decode_qk_pair<G>(p, st, kA, kB, bA >= 0, bB >= 0, jb, ctx, lane, xs);
-        decode_pv_pair<G>(p, st, xs, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
+        decode_pv_pair<G>(p, st, xs, kA, kB, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
       }
     }
   }
@@ -760,7 +883,7 @@ NIA_DEVICE void decode_zero_output(const DecodeParams& p, int b, int hk) {
 // Grid-per-partition variant: grid (max partitions, KV heads, sequences); the
 // partials are merged by paged_decode_combine_kernel.  Used when the batch is
 // too large for the persistent kernel's LDS index.
-template <int G, int PART_BLOCKS>
+template <int G, int PART_BLOCKS, bool FP8>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_bf16_kernel(DecodeParams p) {
   constexpr int BS = 16;
   const int part = blockIdx.x;
@@ -778,7 +901,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_bf16_kernel(Decod
     if (part == 0 && ctx == 0) decode_zero_output<G>(p, b, hk);
     return;
   }
-  decode_bf16_item<G, PART_BLOCKS>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
+  decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
 }
 
 // Largest batch the persistent kernel indexes in LDS (prefix sums of the
@@ -824,9 +947,9 @@ NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
 // launched after this one.  The two counters live at the start of the
 // workspace: they must be zero before the first call, and the last workgroup to
 // leave returns them to zero.
-template <int G, int PART_BLOCKS>
+template <int G, int PART_BLOCKS, bool FP8>
 __global__ __launch_bounds__(kDecodeThreads)
-__attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel(
+__attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
   __shared__ int s_prefix[kPersistentMaxBatch + 1];  // first item number of each sequence
@@ -893,7 +1016,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_bf16_persistent_kernel
     } else {
       int nparts, blk_begin, blk_end;
       decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
-      decode_bf16_item<G, PART_BLOCKS>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
+      decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
     }
     if (tid == 0) s_ticket[(it + 1) & 1] = next;
     __syncthreads();  // next ticket visible; LDS of this item free
@@ -925,12 +1048,12 @@ int32_t decode_max_parts(int32_t max_blocks_per_seq) {
 std::mutex g_occ_mutex;
 std::map<std::pair<int, int>, int> g_occ;
 
-template <int G>
+template <int G, bool FP8>
 int persistent_grid(int device, int upper) {
   int per_cu = 0, cus = 0;
   {
     std::lock_guard<std::mutex> lock(g_occ_mutex);
-    auto it = g_occ.find({device, G});
+    auto it = g_occ.find({device, 2 * G + (FP8 ? 1 : 0)});
     if (it != g_occ.end()) {
       per_cu = it->second & 0xffff;
       cus = it->second >> 16;
@@ -940,17 +1063,18 @@ int persistent_grid(int device, int upper) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
       return -1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, paged_decode_bf16_persistent_kernel<G, kPartBlocks>, kDecodeThreads, 0) !=
+            &per_cu, paged_decode_bf16_persistent_kernel<G, kPartBlocks, FP8>, kDecodeThreads, 0) !=
         hipSuccess)
       return -1;
     if (per_cu < 1) per_cu = 1;
     std::lock_guard<std::mutex> lock(g_occ_mutex);
-    g_occ[{device, G}] = (cus << 16) | per_cu;
+    g_occ[{device, 2 * G + (FP8 ? 1 : 0)}] = (cus << 16) | per_cu;
   }
-  // Two workgroups per CU (8 waves, 16 KB of K/V in flight each) measured faster
-  // than the register-limited maximum of three: the extra streams of random
-  // 4 KB block-heads only add contention in the memory system.
-  const int full = cus * (per_cu < 2 ? per_cu : 2);
+  // bf16: two workgroups per CU (8 waves, 16 KB of K/V in flight each) measured
+  // faster than the register-limited maximum of three, whose extra streams of
+  // random 4 KB block-heads only add contention in the memory system.
+  constexpr int kCap = persistent_waves(G, FP8);
+  const int full = cus * (per_cu < kCap ? per_cu : kCap);
   return upper < full ? upper : full;
 }
 
@@ -963,9 +1087,10 @@ void launch_combine(const DecodeParams& p, int batch, hipStream_t s) {
                      s, p, batch);
 }
 
-template <typename T, int D, int BS>
+template <typename T, int D, int BS, bool FP8 = false>
 int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStream_t s) {
   constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
+  static_assert(kBf16 || !FP8, "fp8 caches take bf16 queries");
   if (kBf16 && batch <= kPersistentMaxBatch) {
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return NIA_ERR_LAUNCH;
@@ -973,9 +1098,9 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
     switch (G) {
 #define NIA_CASE(GG)                                                                          \
   case GG: {                                                                                  \
-    const int grid = persistent_grid<GG>(device, upper);                                      \
+    const int grid = persistent_grid<GG, FP8>(device, upper);                                 \
     if (grid < 1) return NIA_ERR_LAUNCH;                                                      \
-    hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocks>), dim3(grid),    \
+    hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocks, FP8>), dim3(grid), \
                        dim3(kDecodeThreads), 0, s, p, batch, counters);                       \
     break;                                                                                    \
   }
@@ -999,7 +1124,7 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
 #define NIA_CASE(GG)                                                                          \
   case GG:                                                                                    \
     if constexpr (kBf16)                                                                      \
-      hipLaunchKernelGGL((paged_decode_bf16_kernel<GG, kPartBlocks>), grid,                   \
+      hipLaunchKernelGGL((paged_decode_bf16_kernel<GG, kPartBlocks, FP8>), grid,              \
                          dim3(kDecodeThreads), 0, s, p);                                      \
     else                                                                                      \
       hipLaunchKernelGGL((paged_decode_partial_kernel<T, D, GG, BS, kPartBlocks>), grid,      \
@@ -1032,15 +1157,17 @@ extern "C" size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_hea
   return kCounterBytes + (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
 }
 
-extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_stride,
-                                    const void* q, int64_t q_batch_stride, int64_t q_head_stride,
-                                    const void* k_cache, const void* v_cache,
-                                    const int32_t* block_tables, int32_t bt_stride,
-                                    int32_t max_blocks_per_seq, const int64_t* context_lens,
-                                    int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-                                    int32_t head_dim, int32_t block_size, int64_t num_blocks,
-                                    float scale, void* workspace, size_t workspace_bytes,
-                                    int32_t dtype, void* stream) {
+namespace {
+
+int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head_stride,
+                           const void* q, int64_t q_batch_stride, int64_t q_head_stride,
+                           const void* k_cache, const void* v_cache, const float* k_scale,
+                           const float* v_scale, bool fp8, const int32_t* block_tables,
+                           int32_t bt_stride, int32_t max_blocks_per_seq,
+                           const int64_t* context_lens, int32_t batch, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                           int64_t num_blocks, float scale, void* workspace,
+                           size_t workspace_bytes, int32_t dtype, void* stream) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_blocks_per_seq < 0 ||
       bt_stride < max_blocks_per_seq || num_blocks < 0)
     return NIA_ERR_INVALID_ARGUMENT;
@@ -1049,13 +1176,15 @@ extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t
   if (!out || !q || !context_lens || (max_blocks_per_seq > 0 && !block_tables))
     return NIA_ERR_INVALID_ARGUMENT;
   if (max_blocks_per_seq > 0 && (!k_cache || !v_cache)) return NIA_ERR_INVALID_ARGUMENT;
+  if (fp8 && max_blocks_per_seq > 0 && (!k_scale || !v_scale)) return NIA_ERR_INVALID_ARGUMENT;
   const int G = num_heads / num_kv_heads;
   if (head_dim != 128 || block_size != 16 || G > 8) return NIA_ERR_UNSUPPORTED;
-  if (dtype != NIA_DTYPE_BF16 && dtype != NIA_DTYPE_F32) return NIA_ERR_UNSUPPORTED;
+  if (dtype != NIA_DTYPE_BF16 && (fp8 || dtype != NIA_DTYPE_F32)) return NIA_ERR_UNSUPPORTED;
   const int64_t vec = dtype == NIA_DTYPE_BF16 ? 8 : 4;
   if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
       q_batch_stride % vec || q_head_stride % vec)
     return NIA_ERR_MISALIGNED;
+  if (fp8 && ((uintptr_t)k_scale % 4 || (uintptr_t)v_scale % 4)) return NIA_ERR_MISALIGNED;
 
   DecodeParams p;
   p.out = out;
@@ -1066,6 +1195,8 @@ extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t
   p.q_h = q_head_stride;
   p.k_cache = k_cache;
   p.v_cache = v_cache;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
   p.block_tables = block_tables;
   p.bt_stride = bt_stride;
   p.max_blocks = max_blocks_per_seq;
@@ -1085,7 +1216,43 @@ extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t
   p.ws_o = p.ws_ml + (size_t)batch * num_heads * p.max_parts * 2;
 
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NIA_DTYPE_BF16)
-    return launch_decode<bf16_t, 128, 16>(p, G, batch, counters, s);
+  if (fp8) return launch_decode<bf16_t, 128, 16, true>(p, G, batch, counters, s);
+  if (dtype == NIA_DTYPE_BF16) return launch_decode<bf16_t, 128, 16>(p, G, batch, counters, s);
   return launch_decode<float, 128, 16>(p, G, batch, counters, s);
+}
+
+}  // namespace
+
+extern "C" int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_stride,
+                                    const void* q, int64_t q_batch_stride, int64_t q_head_stride,
+                                    const void* k_cache, const void* v_cache,
+                                    const int32_t* block_tables, int32_t bt_stride,
+                                    int32_t max_blocks_per_seq, const int64_t* context_lens,
+                                    int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                    float scale, void* workspace, size_t workspace_bytes,
+                                    int32_t dtype, void* stream) {
+  return paged_decode_entry(out, out_batch_stride, out_head_stride, q, q_batch_stride,
+                            q_head_stride, k_cache, v_cache, nullptr, nullptr, false,
+                            block_tables, bt_stride, max_blocks_per_seq, context_lens, batch,
+                            num_heads, num_kv_heads, head_dim, block_size, num_blocks, scale,
+                            workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride,
+                                        int64_t out_head_stride, const void* q,
+                                        int64_t q_batch_stride, int64_t q_head_stride,
+                                        const void* k_cache, const void* v_cache,
+                                        const float* k_scale, const float* v_scale,
+                                        const int32_t* block_tables, int32_t bt_stride,
+                                        int32_t max_blocks_per_seq, const int64_t* context_lens,
+                                        int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                        float scale, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  return paged_decode_entry(out, out_batch_stride, out_head_stride, q, q_batch_stride,
+                            q_head_stride, k_cache, v_cache, k_scale, v_scale, true,
+                            block_tables, bt_stride, max_blocks_per_seq, context_lens, batch,
+                            num_heads, num_kv_heads, head_dim, block_size, num_blocks, scale,
+                            workspace, workspace_bytes, NIA_DTYPE_BF16, stream);
 }

@@ -18,6 +18,8 @@
 //   of frequency i comes from axis 0 (i < s0), 1 (i < s0 + s1) or 2.
 // The mean's summation order differs from the PyTorch reduction, so a value lying on
 // a rounding boundary can differ in its last bit; everything else is identical.
+// With fp8 caches the rotated k row and the v row are stored as e4m3 codes with one
+// fp32 scale per row (max |x| / 448), as nia_kv_write_fp8 stores them.
 #include "common.h"
 
 namespace {
@@ -39,6 +41,8 @@ struct RopeParams {
   int32_t sec0, sec1;  // mRoPE: frequencies of the temporal and height axes
   void* k_cache;       // one layer [num_blocks][H_kv][BS][128], or null: no write
   void* v_cache;
+  float* k_scale;      // fp8 caches: one scale per row, [num_blocks][H_kv][BS]
+  float* v_scale;
   const int64_t* slots;
   int64_t num_slots;
   int32_t num_tokens, num_heads, num_kv_heads, block_size;
@@ -61,7 +65,21 @@ struct Num<float> {
 
 constexpr int kRows = 4;  // rows (waves) per workgroup
 
-template <typename T>
+// Row maximum of |x| over the wave's 128 values (two per lane).
+NIA_DEVICE float row_amax(float a, float b) {
+  float m = fmaxf(fabsf(a), fabsf(b));
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+  return m;
+}
+
+// e4m3 code of x for a row scale (zero row: scale 0, code 0).
+NIA_DEVICE uint8_t fp8_code(float x, float scale) {
+  return scale > 0.f ? (uint8_t)(fp8x2_from_f32(x / scale, 0.f) & 0xffu) : (uint8_t)0;
+}
+
+// FP8: the caches hold e4m3 codes with one fp32 scale per row, max |x| / 448.
+template <typename T, bool FP8>
 __global__ __launch_bounds__(kRows * kWave) void qk_norm_rope_kernel(RopeParams p) {
   using N = Num<T>;
   constexpr int D = 128;
@@ -101,28 +119,49 @@ __global__ __launch_bounds__(kRows * kWave) void qk_norm_rope_kernel(RopeParams 
     if (slot >= 0 && slot < p.num_slots) {
       const int64_t blk = slot / p.block_size;
       const int off = (int)(slot - blk * p.block_size);
-      const int64_t base = ((blk * p.num_kv_heads + hk) * p.block_size + off) * D;
-      T* kc = reinterpret_cast<T*>(p.k_cache) + base;
-      T* vc = reinterpret_cast<T*>(p.v_cache) + base;
+      const int64_t row_idx = (blk * p.num_kv_heads + hk) * p.block_size + off;
+      const int64_t base = row_idx * D;
       const T* vr = reinterpret_cast<const T*>(p.v) + tok * p.v_tok + (int64_t)hk * p.v_head;
-      kc[lane] = o0;
-      kc[lane + 64] = o1;
-      vc[lane] = vr[lane];
-      vc[lane + 64] = vr[lane + 64];
+      if constexpr (FP8) {
+        const float k0 = N::f(o0), k1 = N::f(o1);
+        const float v0 = N::f(vr[lane]), v1 = N::f(vr[lane + 64]);
+        const float ks = row_amax(k0, k1) / kE4m3Max;
+        const float vs = row_amax(v0, v1) / kE4m3Max;
+        uint8_t* kc = reinterpret_cast<uint8_t*>(p.k_cache) + base;
+        uint8_t* vc = reinterpret_cast<uint8_t*>(p.v_cache) + base;
+        kc[lane] = fp8_code(k0, ks);
+        kc[lane + 64] = fp8_code(k1, ks);
+        vc[lane] = fp8_code(v0, vs);
+        vc[lane + 64] = fp8_code(v1, vs);
+        if (lane == 0) {
+          p.k_scale[row_idx] = ks;
+          p.v_scale[row_idx] = vs;
+        }
+      } else {
+        T* kc = reinterpret_cast<T*>(p.k_cache) + base;
+        T* vc = reinterpret_cast<T*>(p.v_cache) + base;
+        kc[lane] = o0;
+        kc[lane + 64] = o1;
+        vc[lane] = vr[lane];
+        vc[lane + 64] = vr[lane + 64];
+      }
     }
   }
 }
 
 }  // namespace
 
-extern "C" int32_t nia_qk_norm_rope_kv_write(
+namespace {
+
+int32_t launch_qk_norm_rope(
     void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k, int64_t k_tok_stride,
     int64_t k_head_stride, const void* v, int64_t v_tok_stride, int64_t v_head_stride,
     const void* q_norm_weight, const void* k_norm_weight, float eps, const int64_t* positions,
     int64_t pos_axis_stride, int32_t num_axes, const float* inv_freq, int32_t mrope_section0,
-    int32_t mrope_section1, void* k_cache, void* v_cache, const int64_t* slot_mapping,
-    int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream) {
+    int32_t mrope_section1, void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+    bool fp8, const int64_t* slot_mapping, int32_t num_tokens, int32_t num_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int64_t num_blocks,
+    int32_t dtype, void* stream) {
   if (num_tokens < 0 || num_heads < 0 || num_kv_heads < 0) return NIA_ERR_INVALID_ARGUMENT;
   if (num_axes != 1 && num_axes != 3) return NIA_ERR_INVALID_ARGUMENT;
   if (num_axes == 3 && (mrope_section0 < 0 || mrope_section1 < 0 ||
@@ -137,6 +176,7 @@ extern "C" int32_t nia_qk_norm_rope_kv_write(
   if (write && (!v_cache || !v || !slot_mapping || block_size <= 0 || num_blocks < 0 ||
                 num_kv_heads == 0))
     return NIA_ERR_INVALID_ARGUMENT;
+  if (fp8 && (!write || !k_scale || !v_scale)) return NIA_ERR_INVALID_ARGUMENT;
   if (head_dim != 128 || (dtype != NIA_DTYPE_BF16 && dtype != NIA_DTYPE_F32))
     return NIA_ERR_UNSUPPORTED;
   const int64_t rows = (int64_t)num_tokens * (num_heads + num_kv_heads);
@@ -163,6 +203,8 @@ extern "C" int32_t nia_qk_norm_rope_kv_write(
   p.sec1 = mrope_section1;
   p.k_cache = k_cache;
   p.v_cache = v_cache;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
   p.slots = slot_mapping;
   p.num_slots = num_blocks * block_size;
   p.num_tokens = num_tokens;
@@ -170,11 +212,51 @@ extern "C" int32_t nia_qk_norm_rope_kv_write(
   p.num_kv_heads = num_kv_heads;
   p.block_size = block_size;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NIA_DTYPE_BF16)
-    hipLaunchKernelGGL(qk_norm_rope_kernel<bf16_t>, dim3((unsigned)groups), dim3(kRows * kWave),
-                       0, s, p);
-  else
-    hipLaunchKernelGGL(qk_norm_rope_kernel<float>, dim3((unsigned)groups), dim3(kRows * kWave),
-                       0, s, p);
+  const dim3 grid((unsigned)groups), block(kRows * kWave);
+  if (dtype == NIA_DTYPE_BF16) {
+    if (fp8)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<bf16_t, true>), grid, block, 0, s, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<bf16_t, false>), grid, block, 0, s, p);
+  } else {
+    if (fp8)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<float, true>), grid, block, 0, s, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<float, false>), grid, block, 0, s, p);
+  }
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" int32_t nia_qk_norm_rope_kv_write(
+    void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k, int64_t k_tok_stride,
+    int64_t k_head_stride, const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+    const void* q_norm_weight, const void* k_norm_weight, float eps, const int64_t* positions,
+    int64_t pos_axis_stride, int32_t num_axes, const float* inv_freq, int32_t mrope_section0,
+    int32_t mrope_section1, void* k_cache, void* v_cache, const int64_t* slot_mapping,
+    int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream) {
+  return launch_qk_norm_rope(q, q_tok_stride, q_head_stride, k, k_tok_stride, k_head_stride, v,
+                             v_tok_stride, v_head_stride, q_norm_weight, k_norm_weight, eps,
+                             positions, pos_axis_stride, num_axes, inv_freq, mrope_section0,
+                             mrope_section1, k_cache, v_cache, nullptr, nullptr, false,
+                             slot_mapping, num_tokens, num_heads, num_kv_heads, head_dim,
+                             block_size, num_blocks, dtype, stream);
+}
+
+extern "C" int32_t nia_qk_norm_rope_kv_write_fp8(
+    void* q, int64_t q_tok_stride, int64_t q_head_stride, void* k, int64_t k_tok_stride,
+    int64_t k_head_stride, const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+    const void* q_norm_weight, const void* k_norm_weight, float eps, const int64_t* positions,
+    int64_t pos_axis_stride, int32_t num_axes, const float* inv_freq, int32_t mrope_section0,
+    int32_t mrope_section1, void* k_cache, void* v_cache, float* k_scale, float* v_scale,
+    const int64_t* slot_mapping, int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t dtype, void* stream) {
+  return launch_qk_norm_rope(q, q_tok_stride, q_head_stride, k, k_tok_stride, k_head_stride, v,
+                             v_tok_stride, v_head_stride, q_norm_weight, k_norm_weight, eps,
+                             positions, pos_axis_stride, num_axes, inv_freq, mrope_section0,
+                             mrope_section1, k_cache, v_cache, k_scale, v_scale, true,
+                             slot_mapping, num_tokens, num_heads, num_kv_heads, head_dim,
+                             block_size, num_blocks, dtype, stream);
 }

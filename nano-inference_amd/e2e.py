@@ -140,12 +140,20 @@ class Qwen3ForCausalLM(nn.Module):
 
 
 class KVPool:
-    """Paged K/V caches of all layers plus a free list of their blocks."""
+    """Paged K/V caches of all layers plus a free list of their blocks.  With
+    ``fp8`` the caches hold e4m3 codes (uint8) with one fp32 scale per
+    (block, KV head, slot) row in ``k_scale`` / ``v_scale``."""
 
-    def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int, dtype, device):
+    def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int, dtype, device,
+                 fp8: bool = False):
         shape = (cfg.num_layers, num_blocks, cfg.num_kv_heads, block_size, cfg.head_dim)
-        self.k_cache = torch.zeros(shape, dtype=dtype, device=device)
-        self.v_cache = torch.zeros(shape, dtype=dtype, device=device)
+        cdt = torch.uint8 if fp8 else dtype
+        self.k_cache = torch.zeros(shape, dtype=cdt, device=device)
+        self.v_cache = torch.zeros(shape, dtype=cdt, device=device)
+        self.k_scale = self.v_scale = None
+        if fp8:
+            self.k_scale = torch.zeros(shape[:4], dtype=torch.float32, device=device)
+            self.v_scale = torch.zeros(shape[:4], dtype=torch.float32, device=device)
         self.block_size = block_size
         self.free: deque = deque(range(num_blocks))
 
@@ -223,7 +231,8 @@ class Generator:
         dev = self.device
         md = AttentionMetadata(context_lens=lens.to(dev), kv_block_tables=bt.to(dev),
                                slot_mapping=slots.to(dev), k_cache=self.pool.k_cache,
-                               v_cache=self.pool.v_cache, is_prefill=True)
+                               v_cache=self.pool.v_cache, k_scale=self.pool.k_scale,
+                               v_scale=self.pool.v_scale, is_prefill=True)
         return (ids.to(dev), pos.contiguous().to(dev), valid.to(dev), md,
                 (lens - 1).to(dev))
 
@@ -307,7 +316,8 @@ class Generator:
         p, slot, ctx = self._decode_positions()
         md = AttentionMetadata(context_lens=ctx, kv_block_tables=self._bt,
                                slot_mapping=slot.unsqueeze(1), k_cache=self.pool.k_cache,
-                               v_cache=self.pool.v_cache, is_prefill=False)
+                               v_cache=self.pool.v_cache, k_scale=self.pool.k_scale,
+                               v_scale=self.pool.v_scale, is_prefill=False)
         logits = self.model(tok, p.unsqueeze(1), None, md, self._zero)
         nxt = torch.argmax(logits, dim=-1, keepdim=True)
         self._hist.scatter_(1, self._step.expand(self._hist.shape[0], 1), nxt)
@@ -475,7 +485,8 @@ class MixedGenerator:
         slot = self._bt[self._rows, p // bs].to(torch.int64) * bs + p % bs
         md = AttentionMetadata(context_lens=p + 1, kv_block_tables=self._bt,
                                slot_mapping=slot.unsqueeze(1), k_cache=self.pool.k_cache,
-                               v_cache=self.pool.v_cache, is_prefill=False)
+                               v_cache=self.pool.v_cache, k_scale=self.pool.k_scale,
+                               v_scale=self.pool.v_scale, is_prefill=False)
         logits = self.model(tok.unsqueeze(1), p.unsqueeze(1), None, md, self._zero)
         live = self._prod < self.max_new
         dst = torch.where(live, self._sid * self.max_new + self._prod, self._spare)
@@ -559,7 +570,8 @@ class MixedGenerator:
             _lib.check("nia_step_metadata_packed", rc)
             md = PackedAttentionMetadata(
                 context_lens=ctx, kv_block_tables=tables, slot_mapping=slots.unsqueeze(0),
-                k_cache=self.pool.k_cache, v_cache=self.pool.v_cache, is_prefill=nd < b,
+                k_cache=self.pool.k_cache, v_cache=self.pool.v_cache, k_scale=self.pool.k_scale,
+                               v_scale=self.pool.v_scale, is_prefill=nd < b,
                 q_start=q_start, q_len=q_len, num_decode=nd,
                 max_q_len=max((e.n for e in step[nd:]), default=1))
             tail = d[desc.size - 2 * ns:]
@@ -590,15 +602,15 @@ def build(cfg: Optional[Qwen3Config] = None, prompts: Optional[List[List[int]]] 
           max_new_tokens: int = 256, block_size: int = 16, max_prefill_batch: int = 8,
           device: str = "cuda", dtype=torch.bfloat16, seed: int = 4004,
           use_graph: bool = False, mixed: bool = False, max_step_tokens: int = 8192,
-          chunk: int = 1024):
+          chunk: int = 1024, fp8_cache: bool = False):
     """Random-initialised model, a KV pool sized for the prompts, and a generator:
     ``MixedGenerator`` (chunked prefill mixed with decodes) when ``mixed``, else the
-    prefill-first ``Generator``."""
+    prefill-first ``Generator``; ``fp8_cache`` keeps the KV pool in the fp8 format."""
     cfg = cfg or Qwen3Config()
     prompts = prompts if prompts is not None else config4_prompts(seed=seed)
     model = Qwen3ForCausalLM(cfg).init_random(seed).to(device=device, dtype=dtype).eval()
     need = sum(math.ceil((len(p) + max_new_tokens) / block_size) for p in prompts)
-    pool = KVPool(cfg, need + 16, block_size, dtype, torch.device(device))
+    pool = KVPool(cfg, need + 16, block_size, dtype, torch.device(device), fp8=fp8_cache)
     if mixed:
         gen = MixedGenerator(model, pool, max_new_tokens, max_step_tokens, chunk,
                              use_graph=use_graph)
@@ -668,11 +680,13 @@ def main() -> int:
                     help="continuous batching with chunked prefill mixed with decodes")
     ap.add_argument("--step-tokens", type=int, default=8192)
     ap.add_argument("--chunk", type=int, default=1024)
+    ap.add_argument("--fp8-cache", action="store_true", help="KV pool in the fp8 format")
     args = ap.parse_args()
     cfg = Qwen3Config(num_layers=args.layers)
     gen = build(cfg, config4_prompts(args.requests), args.max_new_tokens,
                 max_prefill_batch=args.prefill_batch, use_graph=not args.eager,
-                mixed=args.mixed, max_step_tokens=args.step_tokens, chunk=args.chunk)
+                mixed=args.mixed, max_step_tokens=args.step_tokens, chunk=args.chunk,
+                fp8_cache=args.fp8_cache)
     gen.run([p[:64] for p in gen.prompts[:4]])  # warm-up: kernels, allocator, workspaces
     st = gen.run(gen.prompts)
     line = {"tokens_per_s": round(st.tokens_per_s, 1),

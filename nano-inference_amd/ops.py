@@ -56,18 +56,43 @@ def _default_scale(head_dim: int, scale: Optional[float]) -> float:
 # ---------------------------------------------------------------------------------
 
 
+FP8_CACHE_DTYPES = (torch.uint8, torch.float8_e4m3fn)
+
+
+def is_fp8_cache(cache: torch.Tensor) -> bool:
+    """True for a cache in the fp8 format (e4m3 codes, one fp32 scale per row)."""
+    return cache.dtype in FP8_CACHE_DTYPES
+
+
+def _fp8_scales(k_cache, k_scale, v_scale) -> Tuple[torch.Tensor, torch.Tensor]:
+    if k_scale is None or v_scale is None:
+        raise ValueError("an fp8 cache needs k_scale and v_scale")
+    shape = tuple(k_cache.shape[:3])
+    for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous float32 {shape}")
+        if t.device != k_cache.device:
+            raise ValueError(f"{name} must be on the cache's device")
+    return k_scale, v_scale
+
+
 def kv_write(
     k: torch.Tensor,
     v: torch.Tensor,
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
 ) -> None:
-    """Scatter new K/V rows into one layer's paged cache, in place and bit-exact.
+    """Scatter new K/V rows into one layer's paged cache, in place.
 
     Same effect as the loop at src/nano_inference/layers/attention.py:267-278:
     for every token t with ``slot = slot_mapping[t] >= 0``,
-    ``k_cache[slot // BS, :, slot % BS, :] = k[t]`` (and likewise for v).
+    ``k_cache[slot // BS, :, slot % BS, :] = k[t]`` (and likewise for v), bit-exact.
+    With fp8 caches (uint8 or float8_e4m3fn) each row is stored as e4m3 codes with
+    one fp32 scale in ``k_scale`` / ``v_scale`` [num_blocks, H_kv, BS] (scale =
+    max |x| / 448, code = e4m3(x / scale)).
 
     k, v: (..., H_kv, D) - leading dims are flattened to tokens in the order of
     ``slot_mapping.reshape(-1)``; k_cache, v_cache: [num_blocks, H_kv, BS, D].
@@ -80,7 +105,12 @@ def kv_write(
     nb, hkv, bs, d = k_cache.shape
     if k.shape[-2:] != (hkv, d) or v.shape[-2:] != (hkv, d):
         raise ValueError(f"k/v trailing shape must be ({hkv}, {d}), got {tuple(k.shape)}")
-    if not (k.dtype == v.dtype == k_cache.dtype == v_cache.dtype):
+    fp8 = is_fp8_cache(k_cache)
+    if fp8:
+        if v_cache.dtype != k_cache.dtype or k.dtype != v.dtype:
+            raise ValueError("k and v (and the two caches) must share one dtype")
+        k_scale, v_scale = _fp8_scales(k_cache, k_scale, v_scale)
+    elif not (k.dtype == v.dtype == k_cache.dtype == v_cache.dtype):
         raise ValueError("k, v and the caches must share one dtype")
     if slot_mapping.dtype != torch.int64:
         raise ValueError("slot_mapping must be int64 (the context builder's dtype)")
@@ -93,6 +123,15 @@ def kv_write(
     if slots.numel() != k2.shape[0]:
         raise ValueError(f"{slots.numel()} slots for {k2.shape[0]} tokens")
     lib = _lib.load()
+    if fp8:
+        st = lib.nia_kv_write_fp8(
+            k2.data_ptr(), k2.stride(0), k2.stride(1),
+            v2.data_ptr(), v2.stride(0), v2.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+            slots.data_ptr(), k2.shape[0], hkv, d, bs, nb, dt, _stream(dev),
+        )
+        _lib.check("nia_kv_write_fp8", st)
+        return
     st = lib.nia_kv_write(
         k2.data_ptr(), k2.stride(0), k2.stride(1),
         v2.data_ptr(), v2.stride(0), v2.stride(1),
@@ -143,6 +182,8 @@ def paged_decode(
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """One query token per sequence against its paged keys.
 
@@ -152,6 +193,8 @@ def paged_decode(
     context_lens: (B,) int64.  Returns (B, H, D) (or q's 4-D shape).
     ``workspace`` (optional, uint8) must have been zero before its first use
     (see ``decode_workspace``); by default a cached per-device one is used.
+    fp8 caches (uint8 / float8_e4m3fn codes) take their per-row ``k_scale`` /
+    ``v_scale`` [num_blocks, H_kv, BS] float32 and bf16 queries.
     """
     dev = _require_gpu(q, k_cache, v_cache, block_tables, context_lens)
     squeeze = q.dim() == 4
@@ -173,7 +216,12 @@ def paged_decode(
         raise ValueError(f"head_dim mismatch: q {d}, cache {dc}")
     if h % hkv != 0:
         raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
-    if not (q3.dtype == k_cache.dtype == v_cache.dtype):
+    fp8 = is_fp8_cache(k_cache)
+    if fp8:
+        if v_cache.dtype != k_cache.dtype or q3.dtype != torch.bfloat16:
+            raise ValueError("fp8 caches take bf16 queries (and share one dtype)")
+        k_scale, v_scale = _fp8_scales(k_cache, k_scale, v_scale)
+    elif not (q3.dtype == k_cache.dtype == v_cache.dtype):
         raise ValueError("q and the caches must share one dtype")
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
         raise ValueError("block_tables must be (B, max_blocks) int32")
@@ -200,14 +248,25 @@ def paged_decode(
         raise ValueError(f"decode workspace of {ws_bytes} bytes, {need} needed")
     ws_ptr = workspace.data_ptr()
     lib = _lib.load()
-    st = lib.nia_paged_decode(
-        out3.data_ptr(), out3.stride(0), out3.stride(1),
-        q3.data_ptr(), q3.stride(0), q3.stride(1),
-        k_cache.data_ptr(), v_cache.data_ptr(),
-        block_tables.data_ptr(), block_tables.stride(0), max_blocks, context_lens.data_ptr(),
-        b, h, hkv, d, bs, nb, _default_scale(d, scale), ws_ptr, ws_bytes, dt, _stream(dev),
-    )
-    _lib.check("nia_paged_decode", st)
+    if fp8:
+        st = lib.nia_paged_decode_fp8(
+            out3.data_ptr(), out3.stride(0), out3.stride(1),
+            q3.data_ptr(), q3.stride(0), q3.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), max_blocks, context_lens.data_ptr(),
+            b, h, hkv, d, bs, nb, _default_scale(d, scale), ws_ptr, ws_bytes, _stream(dev),
+        )
+        _lib.check("nia_paged_decode_fp8", st)
+    else:
+        st = lib.nia_paged_decode(
+            out3.data_ptr(), out3.stride(0), out3.stride(1),
+            q3.data_ptr(), q3.stride(0), q3.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), max_blocks,
+            context_lens.data_ptr(), b, h, hkv, d, bs, nb, _default_scale(d, scale), ws_ptr,
+            ws_bytes, dt, _stream(dev),
+        )
+        _lib.check("nia_paged_decode", st)
     if out is not None:
         return out
     return out3.unsqueeze(1) if squeeze else out3
@@ -326,13 +385,20 @@ def prefill_paged(
     causal: int = CAUSAL_BOTTOM_RIGHT,
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Query chunks against their paged keys (nia_prefill_paged).
 
     q/out: (Tq, H, D).  Sequence s has q_len[s] query rows starting at token
     q_start[s], sitting at absolute positions context_lens[s] - q_len[s] + j,
     and reads keys [0, context_lens[s]) through block_tables (B, max_blocks) int32.
+    fp8 caches (with ``k_scale`` / ``v_scale``): the keys are first dequantised into
+    contiguous bf16 rows (nia_dequant_gather_fp8), then attended by nia_prefill.
     """
+    if is_fp8_cache(k_cache):
+        return _prefill_paged_fp8(q, k_cache, v_cache, block_tables, q_start, q_len,
+                                   context_lens, max_q_len, causal, scale, out, k_scale, v_scale)
     dev = _require_gpu(q, k_cache, v_cache, block_tables, q_start, q_len, context_lens)
     if q.dim() != 3:
         raise ValueError("q must be (Tq, H, D)")
@@ -378,6 +444,40 @@ def prefill_paged(
     return out
 
 
+def _prefill_paged_fp8(q, k_cache, v_cache, block_tables, q_start, q_len, context_lens,
+                       max_q_len, causal, scale, out, k_scale, v_scale):
+    dev = _require_gpu(q, k_cache, v_cache, block_tables, q_start, q_len, context_lens)
+    if q.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("q must be (Tq, H, D), caches [num_blocks, H_kv, block_size, D]")
+    if v_cache.dtype != k_cache.dtype or q.dtype != torch.bfloat16:
+        raise ValueError("fp8 caches take bf16 queries (and share one dtype)")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache layer slices must be contiguous")
+    k_scale, v_scale = _fp8_scales(k_cache, k_scale, v_scale)
+    nb, hkv, bs, d = k_cache.shape
+    n = q_start.shape[0]
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != n:
+        raise ValueError("block_tables must be (B, max_blocks) int32")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    if context_lens.dtype != torch.int64 or context_lens.shape != (n,):
+        raise ValueError("context_lens must be (B,) int64")
+    context_lens = context_lens.contiguous()
+    mb = block_tables.shape[1]
+    stride = mb * bs
+    keys = torch.empty((n * stride, hkv, d), dtype=torch.bfloat16, device=dev)
+    vals = torch.empty_like(keys)
+    lib = _lib.load()
+    st = lib.nia_dequant_gather_fp8(
+        k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+        block_tables.data_ptr(), block_tables.stride(0), mb, context_lens.data_ptr(), n, hkv, d,
+        bs, nb, keys.data_ptr(), vals.data_ptr(), stride, _stream(dev))
+    _lib.check("nia_dequant_gather_fp8", st)
+    k_start = torch.arange(n, device=dev, dtype=torch.int32) * stride
+    k_len = context_lens.clamp(0, stride).to(torch.int32)
+    return prefill(q, keys, vals, q_start, q_len, k_start, k_len, max_q_len, causal, scale, out)
+
+
 # ---------------------------------------------------------------------------------
 # Fused QK-RMSNorm + RoPE / mRoPE + KV write
 # ---------------------------------------------------------------------------------
@@ -396,8 +496,11 @@ def qk_norm_rope_kv_write(
     k_cache: Optional[torch.Tensor] = None,
     v_cache: Optional[torch.Tensor] = None,
     slot_mapping: Optional[torch.Tensor] = None,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
 ) -> None:
-    """QK-RMSNorm, RoPE (or mRoPE) in place on q and k, then the KV-cache write.
+    """QK-RMSNorm, RoPE (or mRoPE) in place on q and k, then the KV-cache write
+    (fp8 caches: e4m3 codes plus the per-row ``k_scale`` / ``v_scale``, as kv_write).
 
     Same values as ``q_norm(q)``, ``k_norm(k)``, the rotary module and the write loop
     of src/nano_inference/layers/attention.py:254-278 (every intermediate rounded to
@@ -457,7 +560,12 @@ def qk_norm_rope_kv_write(
             raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, D]")
         if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
             raise ValueError("k_cache/v_cache layer slices must be contiguous")
-        if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        fp8 = is_fp8_cache(k_cache)
+        if fp8:
+            if v_cache.dtype != k_cache.dtype:
+                raise ValueError("k_cache and v_cache must share one dtype")
+            k_scale, v_scale = _fp8_scales(k_cache, k_scale, v_scale)
+        elif k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
             raise ValueError("caches must share the model dtype")
         if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
             raise ValueError(f"slot_mapping must be int64 with {n} entries")
@@ -466,11 +574,16 @@ def qk_norm_rope_kv_write(
         nb, bs = k_cache.shape[0], k_cache.shape[2]
         kc_ptr, vc_ptr, sl_ptr = k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr()
     lib = _lib.load()
-    st = lib.nia_qk_norm_rope_kv_write(
-        q2.data_ptr(), q2.stride(0), q2.stride(1), k2.data_ptr(), k2.stride(0), k2.stride(1),
-        v2.data_ptr(), v2.stride(0), v2.stride(1),
-        qw.data_ptr() if qw is not None else None, kw.data_ptr() if kw is not None else None,
-        float(eps), pos.data_ptr(), pos.stride(0), num_axes, inv.data_ptr(), sec0, sec1,
-        kc_ptr, vc_ptr, sl_ptr, n, q2.shape[1], k2.shape[1], d, bs, nb, dt, _stream(dev),
-    )
+    args = (q2.data_ptr(), q2.stride(0), q2.stride(1), k2.data_ptr(), k2.stride(0), k2.stride(1),
+            v2.data_ptr(), v2.stride(0), v2.stride(1),
+            qw.data_ptr() if qw is not None else None, kw.data_ptr() if kw is not None else None,
+            float(eps), pos.data_ptr(), pos.stride(0), num_axes, inv.data_ptr(), sec0, sec1,
+            kc_ptr, vc_ptr)
+    tail = (sl_ptr, n, q2.shape[1], k2.shape[1], d, bs, nb, dt, _stream(dev))
+    if k_cache is not None and is_fp8_cache(k_cache):
+        st = lib.nia_qk_norm_rope_kv_write_fp8(*args, k_scale.data_ptr(), v_scale.data_ptr(),
+                                               *tail)
+        _lib.check("nia_qk_norm_rope_kv_write_fp8", st)
+        return
+    st = lib.nia_qk_norm_rope_kv_write(*args, *tail)
     _lib.check("nia_qk_norm_rope_kv_write", st)

@@ -94,6 +94,44 @@ class DecodeCase:
         return 4 * self.batch * self.num_kv_heads * self.head_dim * es + 8 * self.batch
 
 
+@dataclass
+class Fp8Cache:
+    """A decode case's cache pool in the fp8 format (e4m3 codes, one scale per row)."""
+
+    k_cache: torch.Tensor  # [layers, NB, H_kv, BS, D] uint8
+    v_cache: torch.Tensor
+    k_scale: torch.Tensor  # [layers, NB, H_kv, BS] float32
+    v_scale: torch.Tensor
+
+
+def quantize_cache_fp8(c: DecodeCase) -> Fp8Cache:
+    """Every row of the case's pool written into fp8 caches by the fp8 KV-write kernel."""
+    from . import ops
+
+    layers, nb, hkv, bs, d = c.k_cache.shape
+    dev = c.k_cache.device
+    out = Fp8Cache(torch.empty((layers, nb, hkv, bs, d), dtype=torch.uint8, device=dev),
+                   torch.empty((layers, nb, hkv, bs, d), dtype=torch.uint8, device=dev),
+                   torch.zeros((layers, nb, hkv, bs), dtype=torch.float32, device=dev),
+                   torch.zeros((layers, nb, hkv, bs), dtype=torch.float32, device=dev))
+    slots = torch.arange(nb * bs, dtype=torch.int64, device=dev)
+    for layer in range(layers):
+        k_rows = c.k_cache[layer].transpose(1, 2).reshape(nb * bs, hkv, d)
+        v_rows = c.v_cache[layer].transpose(1, 2).reshape(nb * bs, hkv, d)
+        ops.kv_write(k_rows, v_rows, out.k_cache[layer], out.v_cache[layer], slots,
+                     out.k_scale[layer], out.v_scale[layer])
+        del k_rows, v_rows
+    return out
+
+
+def fp8_decode_bytes(c: DecodeCase) -> int:
+    """Algorithmic HBM bytes of one decode launch over fp8 caches: K+V codes and row
+    scales, bf16 q + out, tables, lens."""
+    blocks = sum(math.ceil(L / c.block_size) for L in c.lens)
+    return (sum(c.lens) * c.num_kv_heads * (c.head_dim + 4) * 2
+            + 2 * c.batch * c.num_heads * c.head_dim * 2 + 4 * blocks + 8 * c.batch)
+
+
 def make_decode(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                 lens: List[int], pool_blocks: int, block_size: int, dtype, device,
                 seed: int, layers: int = 1, max_blocks: Optional[int] = None,

@@ -122,3 +122,25 @@ def test_mixed_graph_tail_reproduces_eager_tail():
     graph.run(prompts)
     assert graph.outputs == eager.outputs
     check_teacher_forcing(graph, prompts, 9)
+
+
+@pytest.mark.parametrize("mixed", [False, True])
+def test_generation_with_fp8_cache(mixed):
+    """Both generators over an fp8 KV pool.  The prefill-first generator's first token
+    comes from attention over the fresh K/V, so it equals the bf16 pool's exactly; the
+    rest read the fp8 cache (its parity is checked at the layer and kernel level)."""
+    cfg = tiny_config()
+    prompts = e2e.config4_prompts(5, 3, 70, cfg.vocab_size, seed=13)
+    kw = dict(max_new_tokens=6, seed=5, mixed=mixed, max_step_tokens=48, chunk=16)
+    ref_gen = e2e.build(cfg, prompts, **kw)
+    ref_gen.run(prompts)
+    gen = e2e.build(cfg, prompts, fp8_cache=True, **kw)
+    assert gen.pool.k_cache.dtype == torch.uint8
+    free0 = len(gen.pool.free)
+    st = gen.run(prompts)
+    assert st.generated_tokens == len(prompts) * 6
+    assert len(gen.pool.free) == free0
+    for out, ref_out in zip(gen.outputs, ref_gen.outputs):
+        assert len(out) == 6 and all(0 <= t < cfg.vocab_size for t in out)
+        if not mixed:
+            assert out[0] == ref_out[0]
