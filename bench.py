@@ -217,10 +217,10 @@ def bench_decode_vl(torch, ops, workloads):
                          out=out)
 
     warm_up(torch, decode)
-    ms = per_call_ms(torch, decode, 40)
+    ms = time_calls(torch, decode, 30)
     gbps = c.decode_bytes() / (ms * 1e-3) / 1e9
     return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
-                bytes=c.decode_bytes())
+                bytes=c.decode_bytes(), timing="median of 5 batches of 30 back-to-back calls")
 
 
 def bench_decode_fp8(torch, ops, workloads, c):
@@ -235,15 +235,16 @@ def bench_decode_fp8(torch, ops, workloads, c):
                          out=out, k_scale=f8.k_scale[L], v_scale=f8.v_scale[L])
 
     warm_up(torch, decode)
-    ms = per_call_ms(torch, decode, 40)
+    ms = time_calls(torch, decode, 30)
     byts = workloads.fp8_decode_bytes(c)
     gbps = byts / (ms * 1e-3) / 1e9
     del f8
     return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
-                bytes=byts, format="e4m3 codes + fp32 scale per (token, KV head) row")
+                bytes=byts, format="e4m3 codes + fp32 scale per (token, KV head) row",
+                timing="median of 5 batches of 30 back-to-back calls")
 
 
-def bench_e2e(torch, mixed: bool):
+def bench_e2e(torch, mixed: bool, fp8_cache: bool = False):
     """Whole-model generation on the Qwen3-0.6B architecture (random-initialised bf16):
     64 prompts of U[128, 2048] random ids, 256 greedy tokens each.  ``mixed``:
     continuous batching with 1024-token prefill chunks and decodes packed into steps
@@ -252,7 +253,7 @@ def bench_e2e(torch, mixed: bool):
     generated tokens) / elapsed."""
     from nano_inference_amd import e2e
 
-    gen = e2e.build(use_graph=True, mixed=mixed)
+    gen = e2e.build(use_graph=True, mixed=mixed, fp8_cache=fp8_cache)
     gen.run([pr[:64] for pr in gen.prompts[:4]])  # warm-up
     st = gen.run(gen.prompts)
     return dict(tokens_per_s=round(st.tokens_per_s, 1),
@@ -260,7 +261,8 @@ def bench_e2e(torch, mixed: bool):
                 prompt_tokens=st.prompt_tokens, generated_tokens=st.generated_tokens,
                 prefill_s=round(st.prefill_s, 4), decode_s=round(st.decode_s, 4),
                 total_s=round(st.total_s, 4), steps=st.prefill_steps + st.decode_steps,
-                scheduling="chunked prefill mixed with decodes" if mixed else "prefill first")
+                scheduling="chunked prefill mixed with decodes" if mixed else "prefill first",
+                kv_cache="fp8 (e4m3 + row scales)" if fp8_cache else "bf16")
 
 
 def cpu_baseline(torch, workloads, budget_s: float = 20.0):
@@ -374,6 +376,7 @@ def main() -> int:
     if not args.no_e2e:
         extra["e2e_qwen3_0p6b"] = bench_e2e(torch, mixed=True)
         extra["e2e_qwen3_0p6b_prefill_first"] = bench_e2e(torch, mixed=False)
+        extra["e2e_qwen3_0p6b_fp8_cache"] = bench_e2e(torch, mixed=True, fp8_cache=True)
     line = {
         "metric": "decode attn HBM GB/s (% of peak) + prefill attn TFLOP/s (% bf16 MFMA peak)",
         "value": round(value, 1),
