@@ -201,6 +201,13 @@ def bench_prefill(torch, ops, workloads):
 
         ms = time_calls(torch, runv, 30)
         tf = v.flops() / (ms * 1e-3) / 1e12
+        # q, k, v read and the output written once: the windows (about 30 FLOP/B) sit
+        # below the MFMA ridge, so their roofline is HBM bandwidth
+        byts = 4 * v.q.numel() * v.q.element_size()
+        if window:
+            gbps = byts / (ms * 1e-3) / 1e9
+            res[v.name + "_hbm"] = dict(gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
+                                        bytes=byts, bound="hbm")
         res[v.name] = dict(ms=round(ms, 4), tflops=round(tf, 1),
                            frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), chunks=len(v.lens),
                            flops=v.flops())

@@ -420,9 +420,15 @@ NIA_DEVICE s16x4_t lds_read_tr16(const uint8_t* addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)addr);
 }
 
-template <int D, bool PAGED>
+// PAIR (contiguous K/V, no masking, one query head per KV head, sequences of at most
+// 64 queries, e.g. the vision windows): a workgroup takes two heads of one sequence,
+// waves 0-1 the 64 rows of the first and waves 2-3 those of the second, each pair of
+// waves with its own K/V buffer (the two stages), single-buffered.  Half as many
+// workgroups, none of them with idle waves.
+template <int D, bool PAGED, bool PAIR = false>
 __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(PrefillParams p) {
   static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
+  static_assert(!(PAIR && PAGED), "paired heads read contiguous K/V");
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
@@ -435,9 +441,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   const int wave = uniform(tid / kWave);
   const int half = lane >> 5;
   const int col = lane & 31;
+  if constexpr (PAIR) h = 2 * h + (wave >> 1);  // the map numbers head pairs
+  const int wrow = PAIR ? (wave & 1) : wave;    // 32-row group of the m-block
 
   const int qlen = p.q_len[seq];
-  const int m0 = mb * kBlockM;
+  const int m0 = mb * (PAIR ? kBlockM / 2 : kBlockM);
   if (m0 >= qlen) return;
   int klen;
   int64_t kstart = 0;
@@ -458,7 +466,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   if (causal) n_end = min(klen, q_pos0 + min(m0 + kBlockM, qlen));
   if (n_end < 0) n_end = 0;
 
-  const int r0 = m0 + wave * 32;
+  const int r0 = m0 + wrow * 32;
   const int qrow = r0 + col;
   const bool row_ok = qrow < qlen;
   const int kb = causal ? min(klen, q_pos0 + qrow + 1) : klen;
@@ -526,14 +534,14 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       return base + (kstart + row) * tok + (int64_t)hk * head;
     }
   };
-  // DMA this wave's 16 rows of tile n0 (K or V) into `tile` with buffer loads whose
+  // DMA 16-row group `grp` of tile n0 (K or V) into `tile` with buffer loads whose
   // resource spans exactly the 16 rows (a read past it would return zeros, never
   // fault).  Rows past the context repeat the last key (masked later).
   auto issue_rows = [&](const bf16_t* base, int64_t tok, int64_t head, int64_t row_stride,
-                        const uint32_t* lane_off, uint8_t* tile, int n0,
-                        int blk) __attribute__((always_inline)) {
-    uint8_t* dst = tile + wave * 16 * kTileRowBytes;
-    const int g0 = n0 + 16 * wave;
+                        const uint32_t* lane_off, uint8_t* tile, int n0, int blk,
+                        int grp) __attribute__((always_inline)) {
+    uint8_t* dst = tile + grp * 16 * kTileRowBytes;
+    const int g0 = n0 + 16 * grp;
     const int gk = min(g0, klen - 1);
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void*)row_base(base, tok, head, gk, blk), 0, (int)((15 * row_stride + D) * 2),
@@ -554,8 +562,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     }
   };
   auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
-    issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, lds[stage][0], n0, blk);
-    issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, lds[stage][1], n0, blk);
+    issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, lds[stage][0], n0, blk, wave);
+    issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, lds[stage][1], n0, blk, wave);
   };
 
   // ---- per-lane LDS read offsets ---------------------------------------------------------
@@ -672,9 +680,24 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
 
+  if constexpr (PAIR) {
+    // ---- paired heads: each wave pair fills its own buffer (stage = head), one tile at
+    // a time; a wave loads 32 of the tile's 64 rows of K and of V.
+    const int hsel = wave >> 1;
+    for (int n0 = 0; n0 < n_end; n0 += kBlockN) {
+      if (n0 > 0) __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, lds[hsel][0], n0, 0, 2 * wrow + g);
+        issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, lds[hsel][1], n0, 0, 2 * wrow + g);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (n0 < wave_kend) compute_tile(n0, hsel);
+    }
+  } else if (n_end > 0) {
   // ---- main loop: tile n0 in lds[stage] while tile n0 + 64 streams into the other --------
   // Unrolled by two so that each stage's LDS offsets are compile-time constants.
-  if (n_end > 0) {
     int blk_nxt = block_of(0);
     issue_tile(0, 0, blk_nxt);
     if (kBlockN < n_end) blk_nxt = block_of(kBlockN);
@@ -800,6 +823,33 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
   p.groups_per_xcd = (num_seqs * num_kv_heads + kXcds - 1) / kXcds;
   p.causal = causal;
   p.scale_log2 = scale * kLog2e;
+  // Short unmasked sequences with one query head per KV head (the vision windows):
+  // two heads per workgroup, 64 rows each (see prefill_dma_kernel's PAIR mode).
+  if (causal == NIA_CAUSAL_NONE && num_heads == num_kv_heads && num_kv_heads % 2 == 0 &&
+      max_q_len <= kBlockM / 2 && k_tok_stride >= 0 && k_tok_stride < kMaxRowStride &&
+      v_tok_stride >= 0 && v_tok_stride < kMaxRowStride) {
+    p.num_kv_heads = num_kv_heads / 2;  // the workgroup map numbers head pairs
+    p.groups_per_xcd = (num_seqs * p.num_kv_heads + kXcds - 1) / kXcds;
+    p.num_m_blocks = 1;
+    const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd;
+    if (nwg >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t)stream;
+    switch (head_dim) {
+#define NIA_PAIR_CASE(DD)                                                                       \
+  case DD:                                                                                      \
+    hipLaunchKernelGGL((prefill_dma_kernel<DD, false, true>), dim3((unsigned)nwg),              \
+                       dim3(kPrefillThreads), 0, st, p);                                        \
+    break;
+      NIA_PAIR_CASE(64)
+      NIA_PAIR_CASE(80)
+      NIA_PAIR_CASE(96)
+      NIA_PAIR_CASE(128)
+#undef NIA_PAIR_CASE
+      default:
+        return NIA_ERR_UNSUPPORTED;
+    }
+    return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+  }
   return launch_prefill<false>(p, head_dim, num_seqs, (hipStream_t)stream);
 }
 

@@ -67,6 +67,19 @@ def test_varlen_small_full(head_dim, causal, group):
     check_varlen(out, c, "top_left" if causal else "none", what=f"D={head_dim} G={group}")
 
 
+@pytest.mark.parametrize("head_dim", [64, 80, 128])
+@pytest.mark.parametrize("heads", [2, 16])
+def test_short_unmasked_sequences_paired_heads(head_dim, heads):
+    """Sequences of at most 64 rows, no mask, one query head per KV head: the kernel
+    takes two heads per workgroup (every row checked, lengths 1 .. 64)."""
+    lens = [1, 2, 15, 16, 17, 31, 32, 33, 47, 63, 64, 64, 5]
+    c = workloads.make_varlen(lens, heads, heads, head_dim, torch.bfloat16, "cuda",
+                              seed=300 + head_dim + heads, causal=False)
+    out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=False)
+    torch.cuda.synchronize()
+    check_varlen(out, c, "none", what=f"paired heads D={head_dim} H={heads}")
+
+
 def test_vision_full_attention_chunks():
     """7528 patches in 4 images, 16 heads, D 80, non-causal per image (sampled rows)."""
     c = workloads.vision_vl("cuda", window=False)
