@@ -11,18 +11,19 @@ A whole-model throughput harness around the drop-in layers:
 * ``KVPool`` - the reference allocator's cache layout, one
   ``[layers, blocks, kv_heads, block_size, head_dim]`` tensor each for K and V
   (src/nano_inference/kv_cache/allocator.py:35-39), with a free list of blocks.
-* ``Generator`` - continuous batching with prefill priority: waiting prompts
-  enter in prefill steps of up to ``max_prefill_batch`` sequences (padded
-  (B, S_max) batches with a prefix attention mask, as the reference batches
-  prefill), then every running sequence decodes one token per step.  The
-  reference's scheduler gives decode priority instead
-  (src/nano_inference/scheduler/scheduler.py:125-230), which keeps later
-  prompts waiting until earlier requests finish.
-* Step metadata is built as whole-batch tensor operations in the reference's
-  ``AttentionMetadata`` format (src/nano_inference/engine/context_builder.py:
-  120-193): slots ``block[pos // BS] * BS + pos % BS``, -1 for padding; block
-  tables int32 zero-padded; context lengths int64.  Decode steps build theirs on
-  the device from the previous step's, so a decode step makes no host round trip.
+* ``Generator`` - prefill first: waiting prompts enter in prefill steps of up to
+  ``max_prefill_batch`` sequences (padded (B, S_max) batches with a prefix
+  attention mask, as the reference batches prefill), then every running sequence
+  decodes one token per step, the decode step captured once in a HIP graph.
+* ``MixedGenerator`` - continuous batching with chunked prefill: each step packs
+  one token of every decoding sequence and prefill chunks of the others into one
+  row of tokens (``ChunkedScheduler`` plans it; ``PackedAttentionMetadata``
+  routes decode rows to the decode kernel and chunk rows to the chunked-prefill
+  kernel); step metadata is one descriptor expanded on the device, sampled tokens
+  stay on the device, and the all-decode tail replays one HIP graph.  The
+  reference's scheduler runs prefill and decode in separate batches and gives
+  decode priority (src/nano_inference/scheduler/scheduler.py:125-230).
+* Either generator can keep the KV pool in the fp8 format (``fp8_cache``).
 * Sampling is greedy on each sequence's last valid position (the reference takes
   position S_step - 1 of the padded batch for every row,
   src/nano_inference/inferencer/torch_inferencer.py:242-251, which for shorter

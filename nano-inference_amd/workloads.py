@@ -15,6 +15,8 @@ Workloads (head layouts of the models the engine serves):
   prefill_qwen3_8b 8 packed sequences U[256, 4096], 32/8 heads, D 128, bf16
   chunked_qwen3_8b 8 chunks of 512 queries on top of U[0, 8192] cached tokens
   vision_vl       7528 patches of 4 images, 16 heads, D 80, full and window chunks
+quantize_cache_fp8 turns a decode case's pool into the fp8 format (e4m3 codes plus
+one scale per row) with the fp8 KV-write kernel; fp8_decode_bytes counts its bytes.
 """
 from __future__ import annotations
 
