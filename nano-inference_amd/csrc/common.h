@@ -90,6 +90,14 @@ NIA_DEVICE float group_sum(float x) {
 
 NIA_DEVICE bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
+// max(x, x of lane l ^ 32) with v_permlane32_swap (no LDS round trip): the swap of two
+// copies leaves lane l holding x[l % 32] in one and x[l % 32 + 32] in the other.
+NIA_DEVICE float max_xor32(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
 NIA_DEVICE int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // ---- online-softmax merge -----------------------------------------------------

@@ -28,7 +28,10 @@
 //   XOR-swizzled per row (prefill_kernel).  Every O^T register of a
 //   lane belongs to that lane's query, so rescaling O is lane-local.
 // Softmax: exp2 with scale * log2(e) folded into one FMA; the running max is only
-// raised when a tile's max exceeds it by more than 2^8 (lazy rescale).
+// raised when a tile could hold a P above 2^8 (lazy rescale).  prefill_kernel tests
+// the tile's row max; prefill_dma_kernel computes P against the running max first and
+// reduces the row max only when a lane's sum of the tile's P exceeds 2^8 (or the row
+// has no max yet), which keeps the max reduction off the vector unit's common path.
 // Causal tiles above the diagonal are never visited; tiles crossing it are masked.
 // MFMA work per (query, key) pair: 4 * D flops (QK^T and PV).
 #include <type_traits>
@@ -42,6 +45,7 @@ constexpr int kBlockN = 64;
 constexpr int kPrefillWaves = 4;
 constexpr int kPrefillThreads = kPrefillWaves * kWave;
 constexpr float kLazyRescaleP = 8.0f;
+constexpr float kLazyRescaleBound = 256.0f;  // 2^kLazyRescaleP
 
 struct PrefillParams {
   bf16_t* o;
@@ -623,15 +627,42 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
           if (key >= kb) sacc[c][r] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // P against the running max.  The tile's max is only computed (slow path) when the
+    // row has no max yet or a lane's sum of this tile's P exceeds 2^8: every P is at most
+    // its lane's sum, so below that bound no P exceeds 2^8 and the max may stay.
+    uint4 pb[4];
+    float lt = 0.f;  // this lane's sum of the tile's P (bf16, as the P V product uses them)
+    auto exps = [&]() __attribute__((always_inline)) {
+      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+      lt = 0.f;
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float mx2 = mx * p.scale_log2;
-    if (wave_any(mx2 > m_run + kLazyRescaleP)) {
-      const float mn = fmaxf(m_run, mx2);
+        for (int hh = 0; hh < 2; ++hh) {
+          uint32_t w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p0 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub));
+            const float p1 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub));
+            w[j] = pack_bf16x2(p0, p1);
+            lt = dot2_bf16(w[j], kBf16OnePair, lt);
+          }
+          pb[2 * c + hh] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+    };
+    bool slow = wave_any(m_run == -INFINITY);
+    if (!slow) {
+      exps();
+      slow = wave_any(lt > kLazyRescaleBound);
+    }
+    if (slow) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
+      const float mn = fmaxf(m_run, max_xor32(mx) * p.scale_log2);
       const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
       m_run = mn;
       l_run *= corr;
@@ -639,25 +670,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+      exps();
     }
-    const float msub = (m_run == -INFINITY) ? 0.f : m_run;
-    uint4 pb[4];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float p0 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub));
-          const float p1 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub));
-          w[j] = pack_bf16x2(p0, p1);
-          // Row sum of the bf16 probabilities the PV product uses (one dot2 per pair).
-          l_run = dot2_bf16(w[j], kBf16OnePair, l_run);
-        }
-        pb[2 * c + hh] = make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    }
+    l_run += lt;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
