@@ -214,6 +214,30 @@ def bench_prefill(torch, ops, workloads):
     return res
 
 
+def bench_kv_write_prefill(torch, ops, workloads):
+    """KV write at prefill size: the causal prefill workload's K/V (all its tokens, 8 KV
+    heads, D = 128) scattered into a paged cache through a shuffled slot mapping."""
+    c = workloads.prefill_qwen3_8b("cuda")
+    t, hk, d = c.k.shape
+    bs = 16
+    nblk = 2 * ((t + bs - 1) // bs)
+    g = torch.Generator(device="cpu").manual_seed(7)
+    blocks = torch.randperm(nblk, generator=g)[: (t + bs - 1) // bs]
+    pos = torch.arange(t)
+    slots = (blocks[pos // bs] * bs + pos % bs).to(torch.int64).cuda()
+    kc = torch.zeros(nblk, hk, bs, d, dtype=c.k.dtype, device="cuda")
+    vc = torch.zeros_like(kc)
+
+    def run(_):
+        ops.kv_write(c.k, c.v, kc, vc, slots)
+
+    ms = time_calls(torch, run, 50)
+    byts = 4 * t * hk * d * c.k.element_size() + 8 * t
+    return dict(us=round(ms * 1e3, 2), tokens=t, bytes=byts,
+                gbps=round(byts / (ms * 1e-3) / 1e9, 1),
+                frac=round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+
+
 def bench_decode_vl(torch, ops, workloads):
     c = workloads.decode_vl("cuda", layers=DECODE_LAYERS)
     out = torch.empty_like(c.q)
@@ -380,6 +404,7 @@ def main() -> int:
     pf = extra["prefill_qwen3_8b"]
     extra["kv_write_qwen3_8b"] = dict(us=round(wr_ms * 1e3, 2),
                                       gbps=round(c.write_bytes() / (wr_ms * 1e-3) / 1e9, 1))
+    extra["kv_write_prefill_qwen3_8b"] = bench_kv_write_prefill(torch, ops, workloads)
     if not args.no_e2e:
         extra["e2e_qwen3_0p6b"] = bench_e2e(torch, mixed=True)
         extra["e2e_qwen3_0p6b_prefill_first"] = bench_e2e(torch, mixed=False)
