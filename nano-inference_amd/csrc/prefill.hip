@@ -72,6 +72,7 @@ struct PrefillParams {
   int32_t num_m_blocks;
   int32_t num_seqs;
   int32_t groups_per_xcd;  // ceil(num_seqs * num_kv_heads / kXcds)
+  int32_t order_by_len;    // rank-major grid over sequences sorted by key length
   int32_t causal;
   float scale_log2;
 };
@@ -105,6 +106,75 @@ NIA_DEVICE bool prefill_map(const PrefillParams& p, int& seq, int& h, int& mb) {
   return true;
 }
 
+// Rank-major variant, for grids whose workgroups of one sequence all do about the same
+// work (non-causal calls, and chunks after a cached context): sequences are ranked by
+// key length (longest first), the groups of rank r go out before those of rank r + 1
+// on every XCD (a group still lives on one XCD), and a group's m-blocks go out longest
+// first.  Issuing the longest work first keeps a long sequence's workgroups out of the
+// last round of the grid.  s_order[r] is the sequence of rank r.
+constexpr int kOrderMaxSeqs = kPrefillThreads;  // one sequence per thread
+
+NIA_DEVICE bool prefill_map_ranked(const PrefillParams& p, const int* s_order, int& seq, int& h,
+                                   int& mb) {
+  const int id = blockIdx.x;
+  const int x = id % kXcds;
+  const int t = id / kXcds;
+  const int per_j = p.num_m_blocks * p.group;
+  const int j = t / per_j;
+  const int rem = t - j * per_j;
+  const int z = rem / p.group;
+  const int g = rem - z * p.group;
+  const int gid = x + kXcds * j;
+  if (j >= p.groups_per_xcd || gid >= p.num_seqs * p.num_kv_heads) return false;
+  const int r = gid / p.num_kv_heads;
+  seq = s_order[r];
+  h = (gid - r * p.num_kv_heads) * p.group + g;
+  mb = p.num_m_blocks - 1 - z;
+  return true;
+}
+
+// Sequences by descending key length (ties by index) into s_order[0 .. num_seqs), for
+// num_seqs <= kOrderMaxSeqs; every thread of the workgroup takes part.
+template <bool PAGED>
+NIA_DEVICE void rank_sequences(const PrefillParams& p, int* s_key, int* s_order) {
+  const int tid = threadIdx.x;
+  const int n = p.num_seqs;
+  if (tid < n) {
+    int key;
+    if constexpr (PAGED) {
+      const int64_t c = p.ctx_len[tid];
+      const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+      key = (int)(c < 0 ? 0 : (c > cap ? cap : c));
+    } else {
+      key = p.k_len[tid];
+    }
+    s_key[tid] = key;
+  }
+  __syncthreads();
+  if (tid < n) {
+    const int kt = s_key[tid];
+    int r = 0;
+    for (int i = 0; i < n; ++i) {
+      const int ki = s_key[i];
+      r += (ki > kt) || (ki == kt && i < tid);
+    }
+    s_order[r] = tid;
+  }
+  __syncthreads();
+}
+
+// The workgroup's (sequence, head, m-block) under either map.
+template <bool PAGED>
+NIA_DEVICE bool map_workgroup(const PrefillParams& p, int& seq, int& h, int& mb) {
+  if (p.order_by_len) {
+    __shared__ int s_key[kOrderMaxSeqs];
+    __shared__ int s_order[kOrderMaxSeqs];
+    rank_sequences<PAGED>(p, s_key, s_order);
+    return prefill_map_ranked(p, s_order, seq, h, mb);
+  }
+  return prefill_map(p, seq, h, mb);
+}
+
 // XOR swizzle of the 4-key groups inside a transposed-V row (row = head dim d).
 NIA_DEVICE int vt_swz(int d) { return (d ^ (d >> 3)) & 15; }
 
@@ -124,7 +194,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[DP * VT_PITCH];
 
   int seq, h, mb;
-  if (!prefill_map(p, seq, h, mb)) return;
+  if (!map_workgroup<PAGED>(p, seq, h, mb)) return;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -439,7 +509,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2][kTileBytes];  // [stage][K, V]
 
   int seq, h, mb;
-  if (!prefill_map(p, seq, h, mb)) return;
+  if constexpr (PAIR) {
+    if (!prefill_map(p, seq, h, mb)) return;
+  } else {
+    if (!map_workgroup<PAGED>(p, seq, h, mb)) return;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = uniform(tid / kWave);
@@ -838,6 +912,9 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
   p.groups_per_xcd = (num_seqs * num_kv_heads + kXcds - 1) / kXcds;
   p.causal = causal;
   p.scale_log2 = scale * kLog2e;
+  // Every workgroup of a sequence does about the same work unless the mask is the
+  // top-left causal triangle: those grids go out longest sequence first.
+  p.order_by_len = causal != NIA_CAUSAL_TOP_LEFT && num_seqs <= kOrderMaxSeqs;
   // Short unmasked sequences with one query head per KV head (the vision windows):
   // two heads per workgroup, 64 rows each (see prefill_dma_kernel's PAIR mode).
   if (causal == NIA_CAUSAL_NONE && num_heads == num_kv_heads && num_kv_heads % 2 == 0 &&
@@ -920,5 +997,6 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
   p.groups_per_xcd = (num_seqs * num_kv_heads + kXcds - 1) / kXcds;
   p.causal = causal;
   p.scale_log2 = scale * kLog2e;
+  p.order_by_len = causal != NIA_CAUSAL_TOP_LEFT && num_seqs <= kOrderMaxSeqs;
   return launch_prefill<true>(p, head_dim, num_seqs, (hipStream_t)stream);
 }
