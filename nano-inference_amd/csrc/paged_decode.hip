@@ -12,7 +12,8 @@
 //
 // Shapes: D = 128, BS = 16, G = H / H_kv <= 8 (others return NIA_ERR_UNSUPPORTED).
 // bf16 (the serving path)
-//   Work items are (sequence, partition of <= 32 blocks, KV head), numbered on the
+//   Work items are (sequence, partition of <= 32 blocks, or <= 48 when the batch holds
+//   at least 6 items per persistent workgroup, KV head), numbered on the
 //   device from context_lens; persistent workgroups (2 per CU) take them from an
 //   atomic ticket (paged_decode_bf16_persistent_kernel), or the grid enumerates
 //   them for batches above 4096 (paged_decode_bf16_kernel).  An item's 4 waves take
@@ -1034,26 +1035,35 @@ __attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode
 }
 
 constexpr int kPartBlocks = 32;  // 512 tokens per work item at block size 16
+// Longer items when the batch holds at least kLongItemsPerWg of them per persistent
+// workgroup (counted from the block-table width, an upper bound): each item carries a
+// fixed cost (index lookup, table slice, the first loads' latency, the merge of the
+// waves), and with many items per workgroup the longer tail costs less than it saves
+// (Qwen3-8B decode 209 -> 207 us, its fp8 cache 141 -> 135 us; the Qwen2.5-VL batch,
+// about two items per workgroup, keeps 32).
+constexpr int kPartBlocksLong = 48;
+constexpr int kLongItemsPerWg = 6;
 
 // Workspace layout: [work counters (256 B)][m, l per partial][o per partial].
 constexpr size_t kCounterBytes = 256;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-int32_t decode_max_parts(int32_t max_blocks_per_seq) {
-  return (max_blocks_per_seq + kPartBlocks - 1) / kPartBlocks;
+int32_t decode_max_parts(int32_t max_blocks_per_seq, int part_blocks = kPartBlocks) {
+  return (max_blocks_per_seq + part_blocks - 1) / part_blocks;
 }
 
 // Workgroups per CU the persistent kernel reaches, cached per (device, G).
 std::mutex g_occ_mutex;
 std::map<std::pair<int, int>, int> g_occ;
 
-template <int G, bool FP8>
+template <int G, bool FP8, int PB>
 int persistent_grid(int device, int upper) {
   int per_cu = 0, cus = 0;
+  const int key = 4 * G + (FP8 ? 1 : 0) + (PB == kPartBlocks ? 0 : 2);
   {
     std::lock_guard<std::mutex> lock(g_occ_mutex);
-    auto it = g_occ.find({device, 2 * G + (FP8 ? 1 : 0)});
+    auto it = g_occ.find({device, key});
     if (it != g_occ.end()) {
       per_cu = it->second & 0xffff;
       cus = it->second >> 16;
@@ -1063,12 +1073,12 @@ int persistent_grid(int device, int upper) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
       return -1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, paged_decode_bf16_persistent_kernel<G, kPartBlocks, FP8>, kDecodeThreads, 0) !=
+            &per_cu, paged_decode_bf16_persistent_kernel<G, PB, FP8>, kDecodeThreads, 0) !=
         hipSuccess)
       return -1;
     if (per_cu < 1) per_cu = 1;
     std::lock_guard<std::mutex> lock(g_occ_mutex);
-    g_occ[{device, 2 * G + (FP8 ? 1 : 0)}] = (cus << 16) | per_cu;
+    g_occ[{device, key}] = (cus << 16) | per_cu;
   }
   // bf16: two workgroups per CU (8 waves, 16 KB of K/V in flight each) measured
   // faster than the register-limited maximum of three, whose extra streams of
@@ -1078,11 +1088,11 @@ int persistent_grid(int device, int upper) {
   return upper < full ? upper : full;
 }
 
-template <typename T, int D, int BS>
+template <typename T, int D, int BS, int PB = kPartBlocks>
 void launch_combine(const DecodeParams& p, int batch, hipStream_t s) {
   constexpr int kPairsPerGroup = kCombineThreads / kWave;
   const int pairs = batch * p.num_heads;
-  hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, kPartBlocks>),
+  hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, PB>),
                      dim3((pairs + kPairsPerGroup - 1) / kPairsPerGroup), dim3(kCombineThreads), 0,
                      s, p, batch);
 }
@@ -1095,10 +1105,24 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return NIA_ERR_LAUNCH;
     const int upper = batch * p.num_kv_heads * (p.max_parts > 0 ? p.max_parts : 1);
+    // The longer partition: the (m, l) and o partials keep their places in the
+    // workspace, laid out for its smaller partition count.
+    DecodeParams pl = p;
+    pl.max_parts = decode_max_parts(p.max_blocks > 0 ? p.max_blocks : 1, kPartBlocksLong);
+    pl.ws_o = pl.ws_ml + (size_t)batch * p.num_heads * pl.max_parts * 2;
+    const int upper_long = batch * p.num_kv_heads * pl.max_parts;
+    bool long_items = false;
     switch (G) {
 #define NIA_CASE(GG)                                                                          \
   case GG: {                                                                                  \
-    const int grid = persistent_grid<GG, FP8>(device, upper);                                 \
+    const int grid_long = persistent_grid<GG, FP8, kPartBlocksLong>(device, upper_long);      \
+    if (grid_long >= 1 && upper_long >= kLongItemsPerWg * grid_long) {                       \
+      long_items = true;                                                                      \
+      hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocksLong, FP8>),     \
+                         dim3(grid_long), dim3(kDecodeThreads), 0, s, pl, batch, counters);   \
+      break;                                                                                  \
+    }                                                                                         \
+    const int grid = persistent_grid<GG, FP8, kPartBlocks>(device, upper);                    \
     if (grid < 1) return NIA_ERR_LAUNCH;                                                      \
     hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocks, FP8>), dim3(grid), \
                        dim3(kDecodeThreads), 0, s, p, batch, counters);                       \
@@ -1116,7 +1140,11 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
       default:
         return NIA_ERR_UNSUPPORTED;
     }
-    if (p.max_parts > 1) launch_combine<T, D, BS>(p, batch, s);
+    if (long_items) {
+      if (pl.max_parts > 1) launch_combine<T, D, BS, kPartBlocksLong>(pl, batch, s);
+    } else if (p.max_parts > 1) {
+      launch_combine<T, D, BS>(p, batch, s);
+    }
     return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
   }
   const dim3 grid(p.max_parts, p.num_kv_heads, batch);
