@@ -80,6 +80,55 @@ def test_short_unmasked_sequences_paired_heads(head_dim, heads):
     check_varlen(out, c, "none", what=f"paired heads D={head_dim} H={heads}")
 
 
+def test_ranked_grid_ties_and_empty_sequences():
+    """Non-causal calls issue the grid longest sequence first (a rank computed in every
+    workgroup): equal lengths, empty sequences and several m-blocks per sequence, every
+    row checked."""
+    lens = [300, 0, 129, 300, 64, 0, 129, 1, 300, 257]
+    c = workloads.make_varlen(lens, 8, 2, 128, torch.bfloat16, "cuda", seed=910, causal=False)
+    out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=False)
+    torch.cuda.synchronize()
+    check_varlen(out, c, "none", what="ranked grid")
+
+
+def test_more_sequences_than_the_ranking_takes():
+    """301 sequences (the rank holds 256): the grid falls back to the m-block-major map."""
+    g = torch.Generator().manual_seed(911)
+    lens = [int(x) for x in torch.randint(1, 151, (301,), generator=g)]
+    c = workloads.make_varlen(lens, 8, 2, 64, torch.bfloat16, "cuda", seed=912, causal=False)
+    out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=False)
+    torch.cuda.synchronize()
+    check_varlen(out, c, "none", what="301 sequences")
+
+
+def test_bottom_right_contiguous_chunks():
+    """Contiguous K/V longer than the queries (bottom-right mask, ranked grid): query
+    chunks of 1..200 rows on 0..700 earlier keys, and a chunk longer than its keys whose
+    first rows see none (zeros)."""
+    g = torch.Generator().manual_seed(913)
+    ql = [int(x) for x in torch.randint(1, 201, (9,), generator=g)] + [5]
+    kl = [q + int(x) for q, x in zip(ql[:-1], torch.randint(0, 701, (9,), generator=g))] + [2]
+    h, hkv, d = 8, 2, 128
+    tq, tk = sum(ql), sum(kl)
+    q = torch.randn(tq, h, d, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(tk, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(tk, hkv, d, generator=g).to(torch.bfloat16).cuda()
+    qs = torch.tensor([0] + ql[:-1]).cumsum(0).to(torch.int32).cuda()
+    ks = torch.tensor([0] + kl[:-1]).cumsum(0).to(torch.int32).cuda()
+    qlt = torch.tensor(ql, dtype=torch.int32).cuda()
+    klt = torch.tensor(kl, dtype=torch.int32).cuda()
+    out = ops.prefill(q, k, v, qs, qlt, ks, klt, max(ql), ops.CAUSAL_BOTTOM_RIGHT)
+    torch.cuda.synchronize()
+    res = tb.varlen(q.double().cpu().numpy(), k.double().cpu().numpy(),
+                    v.double().cpu().numpy(), qs.cpu().numpy(), ql, ks.cpu().numpy(), kl,
+                    1.0 / math.sqrt(d), "bottom_right")
+    o = out.double().cpu().numpy()
+    got = np.concatenate([o[int(qs[s]) + idx] for s, (idx, _) in res.items()])
+    exp = np.concatenate([ref for _, (_, ref) in res.items()])
+    assert_attn_close(got, exp, torch.bfloat16, "bottom-right contiguous")
+    assert np.all(o[int(qs[-1]):int(qs[-1]) + 3] == 0)
+
+
 def test_vision_full_attention_chunks():
     """7528 patches in 4 images, 16 heads, D 80, non-causal per image (sampled rows)."""
     c = workloads.vision_vl("cuda", window=False)
