@@ -27,11 +27,14 @@
 //   V tile (DMA kernel), or from a transposed V tile whose 4-key groups are
 //   XOR-swizzled per row (prefill_kernel).  Every O^T register of a
 //   lane belongs to that lane's query, so rescaling O is lane-local.
-// Softmax: exp2 with scale * log2(e) folded into one FMA; the running max is only
-// raised when a tile could hold a P above 2^8 (lazy rescale).  prefill_kernel tests
-// the tile's row max; prefill_dma_kernel computes P against the running max first and
-// reduces the row max only when a lane's sum of the tile's P exceeds 2^8 (or the row
-// has no max yet), which keeps the max reduction off the vector unit's common path.
+// Softmax: exp2 of scores in log2 units; the running max is only raised when a tile
+// could hold a P above 2^8 (lazy rescale).  prefill_kernel folds scale * log2(e) and
+// the max into one FMA per score and tests the tile's row max.  prefill_dma_kernel
+// scales Q by scale * log2(e) once (rounded to bf16) and starts each tile's QK chain
+// with the accumulator at minus the running max, so the MFMAs hand over scores that
+// exp2 takes as they are; it computes P against the running max first and reduces
+// the row max only when a lane's sum of the tile's P exceeds 2^8 (or the row has no
+// max yet), which keeps the max reduction off the vector unit's common path.
 // Causal tiles above the diagonal are never visited; tiles crossing it are masked.
 // MFMA work per (query, key) pair: 4 * D flops (QK^T and PV).
 #include <type_traits>
@@ -558,6 +561,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     for (int kk = 0; kk < DK; ++kk)
       qreg[kk] = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk + 8 * half)
                         : make_uint4(0, 0, 0, 0);
+    // Scores in log2 units straight from the MFMAs: q * scale * log2(e), rounded to bf16.
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      uint32_t w[4] = {qreg[kk].x, qreg[kk].y, qreg[kk].z, qreg[kk].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = pack_bf16x2(bf16_lo(w[j]) * p.scale_log2, bf16_hi(w[j]) * p.scale_log2);
+      qreg[kk] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
   }
   f32x16_t oacc[DT];
 #pragma unroll
@@ -566,6 +578,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY;
   float l_run = 0.f;
+  // Initial accumulator of every QK chain: minus the running max (0 before the row has
+  // one), so a tile's scores arrive relative to it.
+  f32x16_t sinit;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sinit[r] = 0.f;
 
   // ---- DMA geometry: instruction i of wave w writes rows 16w + 4i + (lane / 16) ----------
   const int ld_sub = lane >> 4;
@@ -671,17 +688,13 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     const uint8_t* vt = lds[stage][1];
     f32x16_t sacc[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[c][r] = 0.f;
-#pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kTileRowBytes + k_off[kk]);
         sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]), sacc[c], 0,
-            0, 0);
+            __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]),
+            kk == 0 ? sinit : sacc[c], 0, 0, 0);
       }
     }
     // Issue order: K operand reads run six MFMAs ahead.
@@ -693,21 +706,21 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
     if (n0 + kBlockN > wave_kmin) {
+      // key = n0 + 4 half + (32 c + 8 (r / 4) + r % 4) is masked when key >= kb
+      const int lim = kb - n0 - 4 * half;
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = n0 + 32 * c + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (key >= kb) sacc[c][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          if (32 * c + 8 * (r >> 2) + (r & 3) >= lim) sacc[c][r] = -INFINITY;
     }
-    // P against the running max.  The tile's max is only computed (slow path) when the
-    // row has no max yet or a lane's sum of this tile's P exceeds 2^8: every P is at most
-    // its lane's sum, so below that bound no P exceeds 2^8 and the max may stay.
+    // P against the running max (the scores already are relative to it).  The tile's
+    // max is only computed (slow path) when the row has no max yet or a lane's sum of
+    // this tile's P exceeds 2^8: every P is at most its lane's sum, so below that bound
+    // no P exceeds 2^8 and the max may stay.
     uint4 pb[4];
     float lt = 0.f;  // this lane's sum of the tile's P (bf16, as the P V product uses them)
-    auto exps = [&]() __attribute__((always_inline)) {
-      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+    auto exps = [&](auto shifted, float shift) __attribute__((always_inline)) {
       lt = 0.f;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -716,9 +729,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
           uint32_t w[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float p0 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub));
-            const float p1 = fast_exp2(fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub));
-            w[j] = pack_bf16x2(p0, p1);
+            float x0 = sacc[c][8 * hh + 2 * j], x1 = sacc[c][8 * hh + 2 * j + 1];
+            if constexpr (decltype(shifted)::value) {
+              x0 += shift;
+              x1 += shift;
+            }
+            w[j] = pack_bf16x2(fast_exp2(x0), fast_exp2(x1));
             lt = dot2_bf16(w[j], kBf16OnePair, lt);
           }
           pb[2 * c + hh] = make_uint4(w[0], w[1], w[2], w[3]);
@@ -727,7 +743,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     };
     bool slow = wave_any(m_run == -INFINITY);
     if (!slow) {
-      exps();
+      exps(std::false_type(), 0.f);
       slow = wave_any(lt > kLazyRescaleBound);
     }
     if (slow) {
@@ -736,15 +752,20 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
-      const float mn = fmaxf(m_run, max_xor32(mx) * p.scale_log2);
+      // the scores are relative to msub; the new max and its offset are absolute
+      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+      const float mn = fmaxf(m_run, msub + max_xor32(mx));
       const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
       m_run = mn;
+      const float msub_new = (mn == -INFINITY) ? 0.f : mn;
       l_run *= corr;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
-      exps();
+      exps(std::true_type(), msub - msub_new);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sinit[r] = -msub_new;
     }
     l_run += lt;
 #pragma unroll
