@@ -38,6 +38,8 @@ NIA_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+constexpr uint32_t kBf16OnePair = 0x3F803F80u;  // bf16 (1.0, 1.0)
+
 // fp32 += a.lo*b.lo + a.hi*b.hi with bf16 pairs (v_dot2_f32_bf16).
 NIA_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -91,14 +93,50 @@ NIA_DEVICE float group_sum(float x) {
 NIA_DEVICE bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
 // max(x, x of lane l ^ 32) with v_permlane32_swap (no LDS round trip): the swap of two
-// copies leaves lane l holding x[l % 32] in one and x[l % 32 + 32] in the other.
+// copies leaves lane l holding x[l % 32] in one and x[l % 32 + 32] in the other.  The
+// optimizer treats the swap's two results as equal (it folds max(r0, r1) to r0, which
+// keeps lanes 0-31 at their own value), so both pass through an empty asm statement
+// that it cannot see into.
 NIA_DEVICE float max_xor32(float x) {
   const uint32_t u = __builtin_bit_cast(uint32_t, x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+  uint32_t a = r[0], b = r[1];
+  asm("" : "+v"(a), "+v"(b));
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
 NIA_DEVICE int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// ---- LDS ----------------------------------------------------------------------
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element (j % 4)
+// of the 4-element rows addressed by lanes 4r + j / 4, r = 0..3 (a 16x4 <-> 4x16
+// transpose of 16-bit elements).
+NIA_DEVICE s16x4_t lds_read_tr16(const uint8_t* addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)addr);
+}
+
+// Position of 16-byte chunk c of row r in a 256-byte LDS row: c ^ tile_swz(r).  It makes
+// both 16-byte row reads and transposed ds_read_b64_tr_b16 reads of row-major bf16 tiles
+// bank-conflict free.
+NIA_DEVICE int tile_swz(int r) { return ((r & 3) << 2) | ((r & 15) >> 2); }
+
+// ---- global -> LDS DMA --------------------------------------------------------
+
+// Buffer-resource word 3 for raw byte-addressed loads on gfx9-family parts
+// (DATA_FORMAT = 32-bit, all other fields zero).
+constexpr int kBufferWord3 = 0x00020000;
+
+// 16-byte DMA global -> LDS: lane i's 16 bytes at rsrc + voffset land at
+// lds_wave_base + 16 i (a wave-uniform LDS address).  Offsets at or past the
+// resource's size read zeros.
+NIA_DEVICE void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voffset, 0, 0, 0);
+}
 
 // ---- online-softmax merge -----------------------------------------------------
 

@@ -139,42 +139,27 @@ struct Elem<float> {
   static NIA_DEVICE float from_f32(float x) { return x; }
 };
 
-// Merge the per-wave softmax states of a workgroup through LDS and store either
-// the final output (single-partition sequence) or the partition's partial
-// (m, l, un-normalised o) for the combine kernel.  On entry the lanes with
-// row == 0 hold o[g][col * EL .. +EL) and every lane holds the wave's m, l.
-template <typename T, int D, int G, int EL>
-NIA_DEVICE void merge_waves_and_store(const DecodeParams& p, const float (&o)[G][EL],
-                                      const float (&m)[G], const float (&l)[G], int row,
-                                      int col, int wave, int b, int hk, int part, int nparts) {
-  __shared__ float sm_o[kDecodeWaves][G][D];
-  __shared__ float sm_m[kDecodeWaves][G];
-  __shared__ float sm_l[kDecodeWaves][G];
-  if (row == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < EL; ++e) sm_o[wave][g][col * EL + e] = o[g][e];
-      if (col == 0) {
-        sm_m[wave][g] = m[g];
-        sm_l[wave][g] = l[g];
-      }
-    }
-  }
-  __syncthreads();
+// Merge the per-wave softmax states of a workgroup held in LDS and store either the
+// final output (single-partition sequence) or the partition's partial (m, l,
+// un-normalised o) for the combine kernel.  Wave w's o row of head g is at
+// sm_o + w * STRIDE + g * D, its m and l at [w * G + g].  Every thread calls it, after
+// the barrier that follows the stores.
+template <typename T, int D, int G, int STRIDE>
+NIA_DEVICE void merge_lds_and_store(const DecodeParams& p, const float* sm_o, const float* sm_m,
+                                    const float* sm_l, int b, int hk, int part, int nparts) {
   for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads) {
     const int g = idx / D;
     const int d = idx - g * D;
     float mt = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) mt = fmaxf(mt, sm_m[w][g]);
+    for (int w = 0; w < kDecodeWaves; ++w) mt = fmaxf(mt, sm_m[w * G + g]);
     float lt = 0.f, ot = 0.f;
 #pragma unroll
     for (int w = 0; w < kDecodeWaves; ++w) {
-      const float mw = sm_m[w][g];
+      const float mw = sm_m[w * G + g];
       const float wt = (mw == -INFINITY) ? 0.f : fast_exp2(mw - mt);
-      lt = fmaf(sm_l[w][g], wt, lt);
-      ot = fmaf(sm_o[w][g][d], wt, ot);
+      lt = fmaf(sm_l[w * G + g], wt, lt);
+      ot = fmaf(sm_o[w * STRIDE + g * D + d], wt, ot);
     }
     const int h = hk * G + g;
     if (nparts == 1) {
@@ -189,6 +174,30 @@ NIA_DEVICE void merge_waves_and_store(const DecodeParams& p, const float (&o)[G]
       }
     }
   }
+}
+
+// The per-wave states of the vector-unit loops: on entry the lanes with row == 0 hold
+// o[g][col * EL .. +EL) and every lane holds the wave's m, l.
+template <typename T, int D, int G, int EL>
+NIA_DEVICE void merge_waves_and_store(const DecodeParams& p, const float (&o)[G][EL],
+                                      const float (&m)[G], const float (&l)[G], int row,
+                                      int col, int wave, int b, int hk, int part, int nparts) {
+  __shared__ float sm_o[kDecodeWaves * G * D];
+  __shared__ float sm_m[kDecodeWaves * G];
+  __shared__ float sm_l[kDecodeWaves * G];
+  if (row == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < EL; ++e) sm_o[(wave * G + g) * D + col * EL + e] = o[g][e];
+      if (col == 0) {
+        sm_m[wave * G + g] = m[g];
+        sm_l[wave * G + g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  merge_lds_and_store<T, D, G, G * D>(p, sm_o, sm_m, sm_l, b, hk, part, nparts);
 }
 
 template <typename T, int D, int G, int BS, int PART_BLOCKS>
@@ -872,6 +881,229 @@ NIA_DEVICE void decode_item(const DecodeParams& p, int b, int hk, int part, int 
   merge_waves_and_store<bf16_t, D, G>(p, st.o, st.m, st.l, vrow, vc, wave, b, hk, part, nparts);
 }
 
+// ---- matrix-core block loop: query groups of 5 to 8 heads over bf16 caches -----------------
+// The vector-unit loop spends ~100 G instructions per block pair and lane on q . k and
+// P V, which bounds large groups below the memory rate.  Here, per block of 16 keys:
+//   S^T = K Q^T: 4 v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims of K, B = Q^T with the
+//         group's heads in columns 0..G-1 and zeros beyond, scaled by scale * log2 e);
+//   O^T += V^T P^T: 8 v_mfma_f32_16x16x16_bf16, one per 16-dim tile (A = V^T read from
+//         LDS with ds_read_b64_tr_b16, B = P^T, which is the S^T accumulator as it is).
+// In both accumulators lane l owns head l % 16 and rows 4 (l / 16) .. + 3 of the tile, so
+// a head's scores sit in lanes l, l ^ 16, l ^ 32, l ^ 48 and the O rescale is lane-local.
+// The block pairs stream through a 16 KB LDS slot per wave, [K A][V A][K B][V B]: the
+// next pair's DMA is issued as soon as this pair is read out, so a wave holds no
+// registers for loads in flight.  K is placed for its A operand (step j of lane l at
+// 1024 j + 16 l, one ds_read_b128), V row-major with 16-byte chunk c of row r at
+// c ^ tile_swz(r).
+constexpr int kDmaWaveBytes = 16384;
+// Largest batch of this kernel: its sequence index (4 KB) and the four slots (64 KB)
+// keep two workgroups per CU.
+constexpr int kDmaMaxBatch = 1024;
+constexpr bool staged_loop(int G, bool fp8) { return !fp8 && !rolling_loop(G, fp8); }
+
+struct MfmaLaneOffsets {
+  uint32_t k_src[4];  // DMA source offsets in a 4 KB block-head
+  uint32_t v_src[4];
+  int v_read[8];      // transposed read of 16-dim tile mt in the V part
+};
+
+NIA_DEVICE MfmaLaneOffsets mfma_lane_offsets(int lane) {
+  MfmaLaneOffsets o;
+  const int key = lane & 15, quad = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // K: lane l of step j reads key l % 16, dims 32 j + 8 quad .. + 7
+    o.k_src[j] = (uint32_t)(key * 256 + 64 * j + 16 * quad);
+    // V: DMA j fills rows 4 j .. + 3; lane l writes row 4 j + quad at chunk position
+    // l % 16, which holds chunk (l % 16) ^ tile_swz(row)
+    const int r = 4 * j + quad;
+    o.v_src[j] = (uint32_t)(r * 256 + 16 * (key ^ tile_swz(r)));
+  }
+  // ds_read_b64_tr_b16 for the A operand (dim 16 mt + l % 16, keys 4 quad .. + 3): lane
+  // i = 4 rr + q of a 16-lane group addresses row 4 quad + rr, dims 16 mt + 4 q .. + 3.
+  const int i = lane & 15, rr = i >> 2, q = i & 3, row = 4 * quad + rr;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+    o.v_read[mt] = row * 256 + 16 * ((2 * mt + (q >> 1)) ^ tile_swz(row)) + 8 * (q & 1);
+  return o;
+}
+
+// DMA of block-head (blk, hk) of K and V into part (8 KB of a slot).  An invalid block
+// (blk < 0) issues nothing: its scores are masked and its V zeroed after the read.
+NIA_DEVICE void mfma_dma_block(const DecodeParams& p, int blk, int hk, const MfmaLaneOffsets& o,
+                               uint8_t* part) {
+  if (blk < 0) return;
+  // both are wave-uniform (a table entry read by readlane, the item's KV head); saying
+  // so keeps the resources in scalar registers without a waterfall loop
+  blk = uniform(blk);
+  hk = uniform(hk);
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)block_head(p.k_cache, p, blk, hk, 256), 0, 4096, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)block_head(p.v_cache, p, blk, hk, 256), 0, 4096, kBufferWord3);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lds_dma16(kr, o.k_src[j], part + 1024 * j);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lds_dma16(vr, o.v_src[j], part + 4096 + 1024 * j);
+}
+
+template <int G, int PART_BLOCKS>
+NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part, int nparts,
+                                 int blk_begin, int blk_end, int ctx, uint8_t* dma_buf) {
+  constexpr int D = 128;
+  constexpr int BS = 16;
+  static_assert(G <= 16, "the group's heads fill columns of a 16-wide tile");
+  static_assert(PART_BLOCKS <= kWave, "one table entry per lane");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = uniform(threadIdx.x / kWave);
+  const int hn = lane & 15;   // head of the group in this lane's accumulator column
+  const int quad = lane >> 4;
+  const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
+  const int my_bt = (lane < blk_end - blk_begin) ? bt[blk_begin + lane] : -1;
+
+  // B operand of S^T: head hn, dims 32 j + 8 quad .. + 7, times scale * log2(e) (bf16)
+  uint4 qb[4];
+  {
+    const bf16_t* qp = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)b * p.q_b +
+                       (int64_t)(hk * G + (hn < G ? hn : 0)) * p.q_h + 8 * quad;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 u = hn < G ? *reinterpret_cast<const uint4*>(qp + 32 * j) : make_uint4(0, 0, 0, 0);
+      uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = pack_bf16x2(bf16_lo(w[e]) * p.scale_log2, bf16_hi(w[e]) * p.scale_log2);
+      qb[j] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  f32x4_t oacc[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) oacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // the head's running max (the same in its four lanes)
+  float l_run = 0.f;        // this lane's share of the head's sum
+
+  const MfmaLaneOffsets off = mfma_lane_offsets(lane);
+  uint8_t* slot = dma_buf + wave * kDmaWaveBytes;
+  constexpr int kStep = 2 * kDecodeWaves;
+  int jb = blk_begin + 2 * wave;
+  if (jb < blk_end) {
+    int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
+    int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
+    mfma_dma_block(p, bA, hk, off, slot);
+    mfma_dma_block(p, bB, hk, off, slot + 8192);
+    for (;;) {
+      __builtin_amdgcn_s_waitcnt(0);  // this pair is in the slot
+      uint4 ka[2][4];
+      s16x4_t va[2][8];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          ka[x][j] = *reinterpret_cast<const uint4*>(slot + 8192 * x + 1024 * j + 16 * lane);
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) va[x][mt] = lds_read_tr16(slot + 8192 * x + 4096 + off.v_read[mt]);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // read out before the slot is refilled
+      __builtin_amdgcn_sched_barrier(0);
+      const int jn = jb + kStep;
+      const bool more = jn < blk_end;
+      int nA = -1, nB = -1;
+      if (more) {
+        nA = decode_block_id(p, my_bt, jn, blk_begin, blk_end);
+        nB = decode_block_id(p, my_bt, jn + 1, blk_begin, blk_end);
+        mfma_dma_block(p, nA, hk, off, slot);
+        mfma_dma_block(p, nB, hk, off, slot + 8192);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+
+      // ---- scores, masked past the context and in invalid blocks ----------------------------
+      f32x4_t sc[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        sc[x] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sc[x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[x][j]),
+                                                          __builtin_bit_cast(bf16x8_t, qb[j]),
+                                                          sc[x], 0, 0, 0);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const bool ok = x ? bB >= 0 : bA >= 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (!ok || (jb + x) * BS + 4 * quad + i >= ctx) sc[x][i] = -INFINITY;
+      }
+      // ---- lazy running max (raised when a P above 2^8 is possible) -------------------------
+      float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+      bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+      bm = fmaxf(bm, max_xor32(bm));
+      if (wave_any(bm > m_run + kLazyRescale)) {
+        const float mn = fmaxf(m_run, bm);
+        const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
+        m_run = mn;
+        l_run *= corr;
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) oacc[mt] *= corr;
+      }
+      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+      // ---- P^T (keys 4 quad .. + 3 of each block) and O^T += V^T P^T ------------------------
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const uint32_t p01 = pack_bf16x2(fast_exp2(sc[x][0] - msub), fast_exp2(sc[x][1] - msub));
+        const uint32_t p23 = pack_bf16x2(fast_exp2(sc[x][2] - msub), fast_exp2(sc[x][3] - msub));
+        l_run = dot2_bf16(p01, kBf16OnePair, l_run);
+        l_run = dot2_bf16(p23, kBf16OnePair, l_run);
+        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(p01, p23));
+        // V of keys past the context or of an invalid block may be stale (any bits, NaN
+        // included), and 0 * NaN would poison O: zero them.
+        const bool ok = x ? bB >= 0 : bA >= 0;
+        const int key0 = (jb + x) * BS;
+        if (!ok || key0 + BS > ctx) {
+          const int kq = key0 + 4 * quad;
+          const uint32_t m01 = (ok && kq < ctx ? 0xffffu : 0u) | (ok && kq + 1 < ctx ? 0xffff0000u : 0u);
+          const uint32_t m23 = (ok && kq + 2 < ctx ? 0xffffu : 0u) | (ok && kq + 3 < ctx ? 0xffff0000u : 0u);
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt) {
+            uint2 w = __builtin_bit_cast(uint2, va[x][mt]);
+            w.x &= m01;
+            w.y &= m23;
+            va[x][mt] = __builtin_bit_cast(s16x4_t, w);
+          }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)
+          oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[x][mt], pt, oacc[mt], 0, 0, 0);
+      }
+      if (!more) break;
+      bA = nA;
+      bB = nB;
+      jb = jn;
+    }
+  }
+
+  // ---- wave state to LDS (o rows in the wave's own slot, which holds no pending DMA) ------
+  l_run += __shfl_xor(l_run, 16, kWave);
+  l_run += __shfl_xor(l_run, 32, kWave);
+  __shared__ float sm_m[kDecodeWaves * G];
+  __shared__ float sm_l[kDecodeWaves * G];
+  float* sm_o = reinterpret_cast<float*>(dma_buf);
+  constexpr int kStride = kDmaWaveBytes / 4;
+  static_assert(G * D <= kStride, "a wave's o rows fit its slot");
+  if (hn < G) {
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+      *reinterpret_cast<f32x4_t*>(sm_o + wave * kStride + hn * D + 16 * mt + 4 * quad) = oacc[mt];
+    if (quad == 0) {
+      sm_m[wave * G + hn] = m_run;
+      sm_l[wave * G + hn] = l_run;
+    }
+  }
+  __syncthreads();
+  merge_lds_and_store<bf16_t, D, G, kStride>(p, sm_o, sm_m, sm_l, b, hk, part, nparts);
+}
+
 // Zero output rows of a sequence with no keys (all G heads of KV head hk).
 template <int G>
 NIA_DEVICE void decode_zero_output(const DecodeParams& p, int b, int hk) {
@@ -948,12 +1180,18 @@ NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
 // launched after this one.  The two counters live at the start of the
 // workspace: they must be zero before the first call, and the last workgroup to
 // leave returns them to zero.
-template <int G, int PART_BLOCKS, bool FP8>
+template <int G, int PART_BLOCKS, bool FP8, bool DMA = false>
 __global__ __launch_bounds__(kDecodeThreads)
 __attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
-  __shared__ int s_prefix[kPersistentMaxBatch + 1];  // first item number of each sequence
+  constexpr int kMaxBatch = DMA ? kDmaMaxBatch : kPersistentMaxBatch;
+  __shared__ int s_prefix[kMaxBatch + 1];  // first item number of each sequence
+  uint8_t* dma_buf = nullptr;
+  if constexpr (DMA) {
+    __shared__ __attribute__((aligned(1024))) uint8_t s_dma[kDecodeWaves * kDmaWaveBytes];
+    dma_buf = s_dma;
+  }
   __shared__ int s_wave[kDecodeWaves];
   __shared__ int s_ticket[2];
   const int tid = threadIdx.x;
@@ -968,7 +1206,7 @@ __attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode
   // Thread t owns sequences [t * kPer, t * kPer + kPer): their context lengths are
   // loaded together, once, and a workgroup scan of the partition counts gives each
   // sequence's first item number.
-  constexpr int kPer = (kPersistentMaxBatch + kDecodeThreads - 1) / kDecodeThreads;
+  constexpr int kPer = (kMaxBatch + kDecodeThreads - 1) / kDecodeThreads;
   const int b0 = tid * kPer;
   int nparts[kPer];
   int run = 0;
@@ -1017,7 +1255,10 @@ __attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode
     } else {
       int nparts, blk_begin, blk_end;
       decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
-      decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
+      if constexpr (DMA)
+        decode_item_mfma<G, PART_BLOCKS>(p, b, hk, part, nparts, blk_begin, blk_end, ctx, dma_buf);
+      else
+        decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
     }
     if (tid == 0) s_ticket[(it + 1) & 1] = next;
     __syncthreads();  // next ticket visible; LDS of this item free
@@ -1057,10 +1298,10 @@ int32_t decode_max_parts(int32_t max_blocks_per_seq, int part_blocks = kPartBloc
 std::mutex g_occ_mutex;
 std::map<std::pair<int, int>, int> g_occ;
 
-template <int G, bool FP8, int PB>
+template <int G, bool FP8, int PB, bool DMA = false>
 int persistent_grid(int device, int upper) {
   int per_cu = 0, cus = 0;
-  const int key = 4 * G + (FP8 ? 1 : 0) + (PB == kPartBlocks ? 0 : 2);
+  const int key = 8 * G + (DMA ? 4 : 0) + (PB == kPartBlocks ? 0 : 2) + (FP8 ? 1 : 0);
   {
     std::lock_guard<std::mutex> lock(g_occ_mutex);
     auto it = g_occ.find({device, key});
@@ -1073,7 +1314,7 @@ int persistent_grid(int device, int upper) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
       return -1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, paged_decode_bf16_persistent_kernel<G, PB, FP8>, kDecodeThreads, 0) !=
+            &per_cu, paged_decode_bf16_persistent_kernel<G, PB, FP8, DMA>, kDecodeThreads, 0) !=
         hipSuccess)
       return -1;
     if (per_cu < 1) per_cu = 1;
@@ -1097,6 +1338,25 @@ void launch_combine(const DecodeParams& p, int batch, hipStream_t s) {
                      s, p, batch);
 }
 
+// The persistent launch for query group G: longer partitions when the batch holds at
+// least kLongItemsPerWg items per workgroup; DMA selects the LDS-staged block loop.
+template <int G, bool FP8, bool DMA>
+int launch_persistent(const DecodeParams& p, const DecodeParams& pl, int batch, int device,
+                      int upper, int upper_long, int* counters, hipStream_t s, bool& long_items) {
+  const int grid_long = persistent_grid<G, FP8, kPartBlocksLong, DMA>(device, upper_long);
+  if (grid_long >= 1 && upper_long >= kLongItemsPerWg * grid_long) {
+    long_items = true;
+    hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<G, kPartBlocksLong, FP8, DMA>),
+                       dim3(grid_long), dim3(kDecodeThreads), 0, s, pl, batch, counters);
+    return NIA_OK;
+  }
+  const int grid = persistent_grid<G, FP8, kPartBlocks, DMA>(device, upper);
+  if (grid < 1) return NIA_ERR_LAUNCH;
+  hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<G, kPartBlocks, FP8, DMA>), dim3(grid),
+                     dim3(kDecodeThreads), 0, s, p, batch, counters);
+  return NIA_OK;
+}
+
 template <typename T, int D, int BS, bool FP8 = false>
 int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStream_t s) {
   constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
@@ -1111,23 +1371,23 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
     pl.max_parts = decode_max_parts(p.max_blocks > 0 ? p.max_blocks : 1, kPartBlocksLong);
     pl.ws_o = pl.ws_ml + (size_t)batch * p.num_heads * pl.max_parts * 2;
     const int upper_long = batch * p.num_kv_heads * pl.max_parts;
+    // Groups too large for the register pipeline stage their block pairs through LDS.
+    const bool dma = batch <= kDmaMaxBatch;
     bool long_items = false;
+    int rc = NIA_OK;
     switch (G) {
 #define NIA_CASE(GG)                                                                          \
-  case GG: {                                                                                  \
-    const int grid_long = persistent_grid<GG, FP8, kPartBlocksLong>(device, upper_long);      \
-    if (grid_long >= 1 && upper_long >= kLongItemsPerWg * grid_long) {                       \
-      long_items = true;                                                                      \
-      hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocksLong, FP8>),     \
-                         dim3(grid_long), dim3(kDecodeThreads), 0, s, pl, batch, counters);   \
-      break;                                                                                  \
+  case GG:                                                                                    \
+    if constexpr (staged_loop(GG, FP8)) {                                                     \
+      if (dma) {                                                                              \
+        rc = launch_persistent<GG, FP8, true>(p, pl, batch, device, upper, upper_long,        \
+                                              counters, s, long_items);                       \
+        break;                                                                                \
+      }                                                                                       \
     }                                                                                         \
-    const int grid = persistent_grid<GG, FP8, kPartBlocks>(device, upper);                    \
-    if (grid < 1) return NIA_ERR_LAUNCH;                                                      \
-    hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<GG, kPartBlocks, FP8>), dim3(grid), \
-                       dim3(kDecodeThreads), 0, s, p, batch, counters);                       \
-    break;                                                                                    \
-  }
+    rc = launch_persistent<GG, FP8, false>(p, pl, batch, device, upper, upper_long, counters,  \
+                                           s, long_items);                                    \
+    break;
       NIA_CASE(1)
       NIA_CASE(2)
       NIA_CASE(3)
@@ -1140,6 +1400,7 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
       default:
         return NIA_ERR_UNSUPPORTED;
     }
+    if (rc != NIA_OK) return rc;
     if (long_items) {
       if (pl.max_parts > 1) launch_combine<T, D, BS, kPartBlocksLong>(pl, batch, s);
     } else if (p.max_parts > 1) {

@@ -471,31 +471,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
 // ---------------------------------------------------------------------------------
 
 constexpr int kTileRowBytes = 256;                 // 128 bf16
-constexpr uint32_t kBf16OnePair = 0x3F803F80u;     // bf16 (1.0, 1.0)
 constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
 
-NIA_DEVICE int tile_swz(int r) { return ((r & 3) << 2) | ((r & 15) >> 2); }
 
-// Buffer-resource word 3 for raw byte-addressed loads on gfx9-family parts
-// (DATA_FORMAT = 32-bit, all other fields zero).
-constexpr int kBufferWord3 = 0x00020000;
 
-// 16-byte DMA global -> LDS: lane i's 16 bytes at rsrc + voffset land at
-// lds_wave_base + 16 i.
-NIA_DEVICE void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint8_t* lds_wave_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voffset, 0, 0, 0);
-}
-
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef short s16x8_t __attribute__((ext_vector_type(8)));
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element (j % 4)
-// of the 4-element rows addressed by lanes 4r + j / 4, r = 0..3 (a 16x4 <-> 4x16
-// transpose of 16-bit elements).
-NIA_DEVICE s16x4_t lds_read_tr16(const uint8_t* addr) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t*)addr);
-}
 
 // PAIR (contiguous K/V, no masking, one query head per KV head, sequences of at most
 // 64 queries, e.g. the vision windows): a workgroup takes two heads of one sequence,

@@ -101,6 +101,18 @@ def test_long_partitions_at_their_boundaries():
     assert torch.equal(out0[keep], out[keep])
 
 
+@pytest.mark.parametrize("batch", [1024, 1025])
+def test_groups_of_seven_at_the_staged_batch_limit(batch):
+    """Groups of 7 stage their block pairs through LDS up to 1024 sequences and take the
+    plain register loop above; short contexts (1 to 40 tokens) keep the oracle quick."""
+    lens = [int(x) for x in torch.randint(1, 41, (batch,),
+                                          generator=torch.Generator().manual_seed(batch))]
+    c = workloads.make_decode(batch, 28, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",
+                              seed=batch, max_blocks=4)
+    out = run_step(c)
+    assert_attn_close(out, oracle_decode(c), torch.bfloat16, f"G=7 batch {batch}")
+
+
 def test_zero_context_gives_zeros():
     c = workloads.make_decode(3, 8, 2, 128, [5, 40, 600], 64, 16, torch.bfloat16, "cuda", 77)
     ctx = torch.tensor([0, 40, 0], dtype=torch.int64, device="cuda")
@@ -110,9 +122,11 @@ def test_zero_context_gives_zeros():
     assert_attn_close(out[1], oracle_decode(c, seqs=[1])[1], torch.bfloat16, "ctx 40")
 
 
-def test_block_table_permutation_is_bit_invariant():
-    """Moving every block to another physical id (and updating the table) changes nothing."""
-    c = workloads.make_decode(6, 16, 4, 128, [100, 700, 1600, 33, 512, 2049], 1024, 16,
+@pytest.mark.parametrize("heads", [16, 28])
+def test_block_table_permutation_is_bit_invariant(heads):
+    """Moving every block to another physical id (and updating the table) changes nothing
+    (4 KV heads: groups of 4, register pipeline; of 7, block pairs staged through LDS)."""
+    c = workloads.make_decode(6, heads, 4, 128, [100, 700, 1600, 33, 512, 2049], 1024, 16,
                               torch.bfloat16, "cuda", 91)
     out1 = run_step(c)
     perm = torch.randperm(1024, generator=torch.Generator().manual_seed(1)).cuda()
@@ -126,9 +140,12 @@ def test_block_table_permutation_is_bit_invariant():
     assert torch.equal(out1, out2)
 
 
-def test_garbage_past_context_and_in_padding_blocks_is_ignored():
-    """NaN in slots past L (same block) and in block 0 (padded table entries)."""
-    c = workloads.make_decode(4, 8, 2, 128, [20, 33, 48, 100], 64, 16, torch.bfloat16, "cuda", 5)
+@pytest.mark.parametrize("heads", [8, 14])
+def test_garbage_past_context_and_in_padding_blocks_is_ignored(heads):
+    """NaN in slots past L (same block) and in block 0 (padded table entries), for groups
+    of 4 and of 7."""
+    c = workloads.make_decode(4, heads, 2, 128, [20, 33, 48, 100], 64, 16, torch.bfloat16,
+                              "cuda", 5)
     out1 = run_step(c)
     kc, vc = c.k_cache[0], c.v_cache[0]
     used = {b for t in c.tables_list for b in t}
