@@ -1,4 +1,5 @@
-// Split-K paged decode attention for gfx950 (no MFMA: the path is HBM-bound).
+// Split-K paged decode attention for gfx950 (HBM-bound; the matrix cores only take the
+// dot products off the vector unit).
 //
 // Replaces the decode branch of the reference, src/nano_inference/layers/
 // attention.py:285-332: a padded gather of every sequence's K/V through the
@@ -17,13 +18,17 @@
 //   device from context_lens; persistent workgroups (2 per CU) take them from an
 //   atomic ticket (paged_decode_bf16_persistent_kernel), or the grid enumerates
 //   them for batches above 4096 (paged_decode_bf16_kernel).  An item's 4 waves take
-//   the partition's block pairs round-robin.  Per pair a wave issues 16 wave-wide
-//   16-byte loads (K and V of two 4 KB block-heads), and for G <= 4 the next pair's
-//   K goes out right after this pair's scores, its V right after this pair's P V.
-//   K layout: 8 lanes per token, two tokens per lane, so q . k is 8 v_dot2_f32_bf16
-//   plus a 3-step DPP sum.  V layout: 16 lanes per token (8 dims each), so P V is
-//   v_dot2_f32_bf16 over the pair's two blocks with the weights packed as a bf16
-//   pair and moved from the K lanes to the V lanes with ds_bpermute.
+//   the partition's block pairs round-robin.
+//   Batches of at most 1024: decode_item_mfma.  A wave's block pair streams into its
+//   16 KB LDS slot by DMA while the previous pair is computed; scores S^T = K Q^T and
+//   O^T += V^T P^T run on 16x16 MFMAs with the group's heads as columns.
+//   Larger batches (and fp8 caches): decode_item on the vector unit.  Per pair a wave
+//   issues 16 wave-wide 16-byte loads (K and V of two 4 KB block-heads), and for
+//   G <= 4 the next pair's K goes out right after this pair's scores, its V right after
+//   this pair's P V.  K layout: 8 lanes per token, two tokens per lane, so q . k is 8
+//   v_dot2_f32_bf16 plus a 3-step DPP sum.  V layout: 16 lanes per token (8 dims each),
+//   so P V is v_dot2_f32_bf16 over the pair's two blocks with the weights packed as a
+//   bf16 pair and moved from the K lanes to the V lanes with ds_bpermute.
 // fp32 (same shapes)
 //   paged_decode_partial_kernel: grid (partition, KV head, sequence); wave w takes
 //   blocks w, w + 4, ... of the partition; 16 lanes per token in one layout for
@@ -881,9 +886,10 @@ NIA_DEVICE void decode_item(const DecodeParams& p, int b, int hk, int part, int 
   merge_waves_and_store<bf16_t, D, G>(p, st.o, st.m, st.l, vrow, vc, wave, b, hk, part, nparts);
 }
 
-// ---- matrix-core block loop: query groups of 5 to 8 heads over bf16 caches -----------------
-// The vector-unit loop spends ~100 G instructions per block pair and lane on q . k and
-// P V, which bounds large groups below the memory rate.  Here, per block of 16 keys:
+// ---- matrix-core block loop: bf16 caches, batches of at most kDmaMaxBatch -----------------
+// The vector-unit loops spend ~100 G instructions per block pair and lane on q . k and
+// P V, which bounds large groups below the memory rate (Qwen2.5-VL, G = 7: 68.6 us here
+// against 59.7) and costs the Qwen3-8B batch (G = 4) 2%.  Here, per block of 16 keys:
 //   S^T = K Q^T: 4 v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims of K, B = Q^T with the
 //         group's heads in columns 0..G-1 and zeros beyond, scaled by scale * log2 e);
 //   O^T += V^T P^T: 8 v_mfma_f32_16x16x16_bf16, one per 16-dim tile (A = V^T read from
@@ -899,7 +905,7 @@ constexpr int kDmaWaveBytes = 16384;
 // Largest batch of this kernel: its sequence index (4 KB) and the four slots (64 KB)
 // keep two workgroups per CU.
 constexpr int kDmaMaxBatch = 1024;
-constexpr bool staged_loop(int G, bool fp8) { return !fp8 && !rolling_loop(G, fp8); }
+constexpr bool staged_loop(int, bool fp8) { return !fp8; }
 
 struct MfmaLaneOffsets {
   uint32_t k_src[4];  // DMA source offsets in a 4 KB block-head
@@ -1371,7 +1377,7 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
     pl.max_parts = decode_max_parts(p.max_blocks > 0 ? p.max_blocks : 1, kPartBlocksLong);
     pl.ws_o = pl.ws_ml + (size_t)batch * p.num_heads * pl.max_parts * 2;
     const int upper_long = batch * p.num_kv_heads * pl.max_parts;
-    // Groups too large for the register pipeline stage their block pairs through LDS.
+    // bf16 caches: block pairs staged through LDS, scores and P V on the matrix cores.
     const bool dma = batch <= kDmaMaxBatch;
     bool long_items = false;
     int rc = NIA_OK;

@@ -102,15 +102,17 @@ def test_long_partitions_at_their_boundaries():
 
 
 @pytest.mark.parametrize("batch", [1024, 1025])
-def test_groups_of_seven_at_the_staged_batch_limit(batch):
-    """Groups of 7 stage their block pairs through LDS up to 1024 sequences and take the
-    plain register loop above; short contexts (1 to 40 tokens) keep the oracle quick."""
+@pytest.mark.parametrize("heads", [16, 28])
+def test_groups_at_the_staged_batch_limit(heads, batch):
+    """bf16 batches of up to 1024 sequences run the matrix-core loop (block pairs staged
+    through LDS); above it groups of 4 take the register pipeline and groups of 7 the
+    plain vector loop.  Short contexts (1 to 40 tokens) keep the oracle quick."""
     lens = [int(x) for x in torch.randint(1, 41, (batch,),
                                           generator=torch.Generator().manual_seed(batch))]
-    c = workloads.make_decode(batch, 28, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",
+    c = workloads.make_decode(batch, heads, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",
                               seed=batch, max_blocks=4)
     out = run_step(c)
-    assert_attn_close(out, oracle_decode(c), torch.bfloat16, f"G=7 batch {batch}")
+    assert_attn_close(out, oracle_decode(c), torch.bfloat16, f"G={heads // 4} batch {batch}")
 
 
 def test_zero_context_gives_zeros():
