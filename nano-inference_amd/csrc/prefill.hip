@@ -540,7 +540,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     for (int kk = 0; kk < DK; ++kk)
       qreg[kk] = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk + 8 * half)
                         : make_uint4(0, 0, 0, 0);
-    // Scores in log2 units straight from the MFMAs: q * scale * log2(e), rounded to bf16.
+  }
+  // Scores in log2 units straight from the MFMAs: q * scale * log2(e), rounded to bf16
+  // (not for paired heads).  Called once the first K/V tile's DMA is out, so that Q's
+  // load latency overlaps it.
+  auto scale_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
       uint32_t w[4] = {qreg[kk].x, qreg[kk].y, qreg[kk].z, qreg[kk].w};
@@ -549,7 +553,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         w[j] = pack_bf16x2(bf16_lo(w[j]) * p.scale_log2, bf16_hi(w[j]) * p.scale_log2);
       qreg[kk] = make_uint4(w[0], w[1], w[2], w[3]);
     }
-  }
+  };
   f32x16_t oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -671,9 +675,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kTileRowBytes + k_off[kk]);
+        // paired heads: scores are absolute, the chain starts from zero
         sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]),
-            kk == 0 ? sinit : sacc[c], 0, 0, 0);
+            kk == 0 ? (PAIR ? f32x16_t{} : sinit) : sacc[c], 0, 0, 0);
       }
     }
     // Issue order: K operand reads run six MFMAs ahead.
@@ -699,6 +704,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     // no P exceeds 2^8 and the max may stay.
     uint4 pb[4];
     float lt = 0.f;  // this lane's sum of the tile's P (bf16, as the P V product uses them)
+    // Paired heads (windows of one tile, which always take the slow path) keep Q unscaled
+    // and fold scale * log2(e) and the max into one FMA per score, as scaling Q would
+    // only add to their short critical path.
     auto exps = [&](auto shifted, float shift) __attribute__((always_inline)) {
       lt = 0.f;
 #pragma unroll
@@ -709,7 +717,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float x0 = sacc[c][8 * hh + 2 * j], x1 = sacc[c][8 * hh + 2 * j + 1];
-            if constexpr (decltype(shifted)::value) {
+            if constexpr (PAIR) {
+              x0 = fmaf(x0, p.scale_log2, shift);
+              x1 = fmaf(x1, p.scale_log2, shift);
+            } else if constexpr (decltype(shifted)::value) {
               x0 += shift;
               x1 += shift;
             }
@@ -722,7 +733,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     };
     bool slow = wave_any(m_run == -INFINITY);
     if (!slow) {
-      exps(std::false_type(), 0.f);
+      exps(std::false_type(), PAIR ? -m_run : 0.f);  // m_run is finite here
       slow = wave_any(lt > kLazyRescaleBound);
     }
     if (slow) {
@@ -731,9 +742,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
-      // the scores are relative to msub; the new max and its offset are absolute
+      // the scores are relative to msub (unscaled absolute ones for paired heads); the
+      // new max and its offset are absolute
       const float msub = (m_run == -INFINITY) ? 0.f : m_run;
-      const float mn = fmaxf(m_run, msub + max_xor32(mx));
+      const float mn =
+          fmaxf(m_run, PAIR ? max_xor32(mx) * p.scale_log2 : msub + max_xor32(mx));
       const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
       m_run = mn;
       const float msub_new = (mn == -INFINITY) ? 0.f : mn;
@@ -742,9 +755,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
-      exps(std::true_type(), msub - msub_new);
+      exps(std::true_type(), PAIR ? -msub_new : msub - msub_new);
+      if constexpr (!PAIR) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sinit[r] = -msub_new;
+        for (int r = 0; r < 16; ++r) sinit[r] = -msub_new;
+      }
     }
     l_run += lt;
 #pragma unroll
@@ -789,6 +804,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   // Unrolled by two so that each stage's LDS offsets are compile-time constants.
     int blk_nxt = block_of(0);
     issue_tile(0, 0, blk_nxt);
+    scale_q();
     if (kBlockN < n_end) blk_nxt = block_of(kBlockN);
     auto step = [&](int n0, auto stage_c) __attribute__((always_inline)) {
       constexpr int kStage = decltype(stage_c)::value;
