@@ -905,7 +905,7 @@ constexpr int kDmaWaveBytes = 16384;
 // Largest batch of this kernel: its sequence index (4 KB) and the four slots (64 KB)
 // keep two workgroups per CU.
 constexpr int kDmaMaxBatch = 1024;
-constexpr bool staged_loop(int, bool fp8) { return !fp8; }
+constexpr bool staged_loop(int, bool) { return true; }
 
 struct MfmaLaneOffsets {
   uint32_t k_src[4];  // DMA source offsets in a 4 KB block-head
@@ -953,7 +953,34 @@ NIA_DEVICE void mfma_dma_block(const DecodeParams& p, int blk, int hk, const Mfm
   for (int j = 0; j < 4; ++j) lds_dma16(vr, o.v_src[j], part + 4096 + 1024 * j);
 }
 
-template <int G, int PART_BLOCKS>
+// fp8 caches: a block part (8 KB of the slot) holds [K codes 2 KB][V codes 2 KB][V bf16 4 KB].
+// K: DMA d of lane l brings key l % 16, codes of dims 64 d + 16 quad .. + 15, to 1024 d + 16 l;
+// they feed QK steps 2 d (first 8 dims) and 2 d + 1 (last 8), and Q is laid out the same way.
+// V: the codes are copied as they are; each lane widens 16 of them (row 8 d + l / 8, dims
+// 16 (l % 8) .. + 15) into the bf16 part, row-major with the chunk swizzle, for the transposed
+// reads of the bf16 loop.
+NIA_DEVICE void mfma_dma_block_fp8(const DecodeParams& p, int blk, int hk, int lane, uint8_t* part) {
+  if (blk < 0) return;
+  blk = uniform(blk);
+  hk = uniform(hk);
+  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)block_head(p.k_cache, p, blk, hk, 128), 0, 2048, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)block_head(p.v_cache, p, blk, hk, 128), 0, 2048, kBufferWord3);
+  const uint32_t ksrc = (uint32_t)((lane & 15) * 128 + 16 * (lane >> 4));
+#pragma unroll
+  for (int d = 0; d < 2; ++d) lds_dma16(kr, ksrc + 64u * d, part + 1024 * d);
+#pragma unroll
+  for (int d = 0; d < 2; ++d) lds_dma16(vr, 16u * lane + 1024u * d, part + 2048 + 1024 * d);
+}
+
+// 8 e4m3 codes (two dwords) -> 8 bf16 (exact).
+NIA_DEVICE uint4 widen_fp8x8(uint32_t a, uint32_t b) {
+  return make_uint4(bf16x2_from_fp8x2<false>(a), bf16x2_from_fp8x2<true>(a),
+                    bf16x2_from_fp8x2<false>(b), bf16x2_from_fp8x2<true>(b));
+}
+
+template <int G, int PART_BLOCKS, bool FP8 = false>
 NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part, int nparts,
                                  int blk_begin, int blk_end, int ctx, uint8_t* dma_buf) {
   constexpr int D = 128;
@@ -967,14 +994,16 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
   const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
   const int my_bt = (lane < blk_end - blk_begin) ? bt[blk_begin + lane] : -1;
 
-  // B operand of S^T: head hn, dims 32 j + 8 quad .. + 7, times scale * log2(e) (bf16)
+  // B operand of S^T: head hn, dims 32 j + 8 quad .. + 7 (fp8: 64 (j / 2) + 16 quad + 8 (j % 2)
+  // .. + 7, the order of the K codes), times scale * log2(e) (bf16)
   uint4 qb[4];
   {
     const bf16_t* qp = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)b * p.q_b +
-                       (int64_t)(hk * G + (hn < G ? hn : 0)) * p.q_h + 8 * quad;
+                       (int64_t)(hk * G + (hn < G ? hn : 0)) * p.q_h;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint4 u = hn < G ? *reinterpret_cast<const uint4*>(qp + 32 * j) : make_uint4(0, 0, 0, 0);
+      const int d0 = FP8 ? 64 * (j >> 1) + 16 * quad + 8 * (j & 1) : 32 * j + 8 * quad;
+      const uint4 u = hn < G ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
       uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -995,20 +1024,55 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
   if (jb < blk_end) {
     int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
     int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
-    mfma_dma_block(p, bA, hk, off, slot);
-    mfma_dma_block(p, bB, hk, off, slot + 8192);
+    // fp8: the row scales of the pair's keys 4 quad .. + 3 (zeros for an invalid block)
+    float4 ks[2], vs[2];
+    auto issue = [&](int x, int blk) __attribute__((always_inline)) {
+      if constexpr (FP8) {
+        mfma_dma_block_fp8(p, blk, hk, lane, slot + 8192 * x);
+        const int64_t row0 = ((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) * 16 + 4 * quad;
+        ks[x] = blk >= 0 ? *reinterpret_cast<const float4*>(p.k_scale + row0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        vs[x] = blk >= 0 ? *reinterpret_cast<const float4*>(p.v_scale + row0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        mfma_dma_block(p, blk, hk, off, slot + 8192 * x);
+      }
+    };
+    issue(0, bA);
+    issue(1, bB);
     for (;;) {
       __builtin_amdgcn_s_waitcnt(0);  // this pair is in the slot
       uint4 ka[2][4];
       s16x4_t va[2][8];
+      float4 ksc[2], vsc[2];  // this pair's scales (fp8)
+      if constexpr (FP8) {
+        // widen V into the bf16 parts (each wave its own slot: no barrier), K into registers
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
+        for (int x = 0; x < 2; ++x) {
+          ksc[x] = ks[x];
+          vsc[x] = vs[x];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          ka[x][j] = *reinterpret_cast<const uint4*>(slot + 8192 * x + 1024 * j + 16 * lane);
+          for (int d = 0; d < 2; ++d) {
+            const uint4 kc = *reinterpret_cast<const uint4*>(slot + 8192 * x + 1024 * d + 16 * lane);
+            ka[x][2 * d] = widen_fp8x8(kc.x, kc.y);
+            ka[x][2 * d + 1] = widen_fp8x8(kc.z, kc.w);
+            const uint4 vc = *reinterpret_cast<const uint4*>(slot + 8192 * x + 2048 + 1024 * d + 16 * lane);
+            const int r = 8 * d + (lane >> 3), c = 2 * (lane & 7);
+            uint8_t* vrow = slot + 8192 * x + 4096 + r * 256;
+            *reinterpret_cast<uint4*>(vrow + 16 * (c ^ tile_swz(r))) = widen_fp8x8(vc.x, vc.y);
+            *reinterpret_cast<uint4*>(vrow + 16 * ((c + 1) ^ tile_swz(r))) = widen_fp8x8(vc.z, vc.w);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // the widened V rows are in place
+      } else {
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            ka[x][j] = *reinterpret_cast<const uint4*>(slot + 8192 * x + 1024 * j + 16 * lane);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) va[x][mt] = lds_read_tr16(slot + 8192 * x + 4096 + off.v_read[mt]);
-      }
       __builtin_amdgcn_s_waitcnt(0);  // read out before the slot is refilled
       __builtin_amdgcn_sched_barrier(0);
       const int jn = jb + kStep;
@@ -1017,8 +1081,8 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
       if (more) {
         nA = decode_block_id(p, my_bt, jn, blk_begin, blk_end);
         nB = decode_block_id(p, my_bt, jn + 1, blk_begin, blk_end);
-        mfma_dma_block(p, nA, hk, off, slot);
-        mfma_dma_block(p, nB, hk, off, slot + 8192);
+        issue(0, nA);
+        issue(1, nB);
       }
       __builtin_amdgcn_sched_barrier(0);
 
@@ -1035,6 +1099,12 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
       }
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
+        if constexpr (FP8) {
+          sc[x][0] *= ksc[x].x;
+          sc[x][1] *= ksc[x].y;
+          sc[x][2] *= ksc[x].z;
+          sc[x][3] *= ksc[x].w;
+        }
         const bool ok = x ? bB >= 0 : bA >= 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -1057,15 +1127,26 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
       // ---- P^T (keys 4 quad .. + 3 of each block) and O^T += V^T P^T ------------------------
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
-        const uint32_t p01 = pack_bf16x2(fast_exp2(sc[x][0] - msub), fast_exp2(sc[x][1] - msub));
-        const uint32_t p23 = pack_bf16x2(fast_exp2(sc[x][2] - msub), fast_exp2(sc[x][3] - msub));
-        l_run = dot2_bf16(p01, kBf16OnePair, l_run);
-        l_run = dot2_bf16(p23, kBf16OnePair, l_run);
-        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(p01, p23));
         // V of keys past the context or of an invalid block may be stale (any bits, NaN
-        // included), and 0 * NaN would poison O: zero them.
+        // included), and 0 * NaN would poison O: zero them (and their fp8 row scales).
         const bool ok = x ? bB >= 0 : bA >= 0;
         const int key0 = (jb + x) * BS;
+        uint32_t p01, p23;
+        if constexpr (FP8) {
+          const int kq = key0 + 4 * quad;
+          const float e0 = fast_exp2(sc[x][0] - msub), e1 = fast_exp2(sc[x][1] - msub);
+          const float e2 = fast_exp2(sc[x][2] - msub), e3 = fast_exp2(sc[x][3] - msub);
+          l_run += (e0 + e1) + (e2 + e3);
+          // the weights that multiply the V codes carry the rows' v scales
+          p01 = pack_bf16x2(e0 * (ok && kq < ctx ? vsc[x].x : 0.f), e1 * (ok && kq + 1 < ctx ? vsc[x].y : 0.f));
+          p23 = pack_bf16x2(e2 * (ok && kq + 2 < ctx ? vsc[x].z : 0.f), e3 * (ok && kq + 3 < ctx ? vsc[x].w : 0.f));
+        } else {
+          p01 = pack_bf16x2(fast_exp2(sc[x][0] - msub), fast_exp2(sc[x][1] - msub));
+          p23 = pack_bf16x2(fast_exp2(sc[x][2] - msub), fast_exp2(sc[x][3] - msub));
+          l_run = dot2_bf16(p01, kBf16OnePair, l_run);
+          l_run = dot2_bf16(p23, kBf16OnePair, l_run);
+        }
+        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(p01, p23));
         if (!ok || key0 + BS > ctx) {
           const int kq = key0 + 4 * quad;
           const uint32_t m01 = (ok && kq < ctx ? 0xffffu : 0u) | (ok && kq + 1 < ctx ? 0xffff0000u : 0u);
@@ -1188,7 +1269,7 @@ NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
 // leave returns them to zero.
 template <int G, int PART_BLOCKS, bool FP8, bool DMA = false>
 __global__ __launch_bounds__(kDecodeThreads)
-__attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode_bf16_persistent_kernel(
+__attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8 && !DMA)))) void paged_decode_bf16_persistent_kernel(
     DecodeParams p, int batch, int* counters) {
   constexpr int BS = 16;
   constexpr int kMaxBatch = DMA ? kDmaMaxBatch : kPersistentMaxBatch;
@@ -1262,7 +1343,8 @@ __attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8)))) void paged_decode
       int nparts, blk_begin, blk_end;
       decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
       if constexpr (DMA)
-        decode_item_mfma<G, PART_BLOCKS>(p, b, hk, part, nparts, blk_begin, blk_end, ctx, dma_buf);
+        decode_item_mfma<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx,
+                                              dma_buf);
       else
         decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
     }
@@ -1330,7 +1412,7 @@ int persistent_grid(int device, int upper) {
   // bf16: two workgroups per CU (8 waves, 16 KB of K/V in flight each) measured
   // faster than the register-limited maximum of three, whose extra streams of
   // random 4 KB block-heads only add contention in the memory system.
-  constexpr int kCap = persistent_waves(G, FP8);
+  constexpr int kCap = persistent_waves(G, FP8 && !DMA);
   const int full = cus * (per_cu < kCap ? per_cu : kCap);
   return upper < full ? upper : full;
 }
