@@ -149,6 +149,21 @@ def test_decode_fp8_group_sizes(g):
     assert_attn_close(run_fp8(c, f8), oracle_decode_fp8(c, f8), torch.bfloat16, f"fp8 G={g}")
 
 
+@pytest.mark.parametrize("batch", [1024, 1025])
+@pytest.mark.parametrize("heads", [16, 28])
+def test_decode_fp8_at_the_staged_batch_limit(heads, batch):
+    """fp8 batches of up to 1024 sequences run the matrix-core loop (codes staged through
+    LDS); above it groups of 4 take the vector loop at three workgroups per CU and groups
+    of 7 the plain vector loop.  Short contexts (1 to 40 tokens) keep the oracle quick."""
+    lens = [int(x) for x in torch.randint(1, 41, (batch,),
+                                          generator=torch.Generator().manual_seed(batch + 7))]
+    c = workloads.make_decode(batch, heads, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",
+                              seed=batch + 7, max_blocks=4)
+    f8 = workloads.quantize_cache_fp8(c)
+    assert_attn_close(run_fp8(c, f8), oracle_decode_fp8(c, f8), torch.bfloat16,
+                      f"fp8 G={heads // 4} batch {batch}")
+
+
 def test_decode_fp8_qwen3_8b_sampled_rows():
     """The 64-sequence Qwen3-8B workload; every row checked on 12 sequences."""
     c = workloads.decode_qwen3_8b("cuda")
