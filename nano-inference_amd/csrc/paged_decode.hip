@@ -19,10 +19,11 @@
 //   atomic ticket (paged_decode_bf16_persistent_kernel), or the grid enumerates
 //   them for batches above 4096 (paged_decode_bf16_kernel).  An item's 4 waves take
 //   the partition's block pairs round-robin.
-//   Batches of at most 1024: decode_item_mfma.  A wave's block pair streams into its
-//   16 KB LDS slot by DMA while the previous pair is computed; scores S^T = K Q^T and
-//   O^T += V^T P^T run on 16x16 MFMAs with the group's heads as columns.
-//   Larger batches (and fp8 caches): decode_item on the vector unit.  Per pair a wave
+//   Batches of at most 1024 (bf16 and fp8 caches): decode_item_mfma.  A wave's block
+//   pair streams into its 16 KB LDS slot by DMA while the previous pair is computed;
+//   scores S^T = K Q^T and O^T += V^T P^T run on 16x16 MFMAs with the group's heads as
+//   columns.
+//   Larger batches: decode_item on the vector unit.  Per pair a wave
 //   issues 16 wave-wide 16-byte loads (K and V of two 4 KB block-heads), and for
 //   G <= 4 the next pair's K goes out right after this pair's scores, its V right after
 //   this pair's P V.  K layout: 8 lanes per token, two tokens per lane, so q . k is 8
@@ -886,7 +887,7 @@ NIA_DEVICE void decode_item(const DecodeParams& p, int b, int hk, int part, int 
   merge_waves_and_store<bf16_t, D, G>(p, st.o, st.m, st.l, vrow, vc, wave, b, hk, part, nparts);
 }
 
-// ---- matrix-core block loop: bf16 caches, batches of at most kDmaMaxBatch -----------------
+// ---- matrix-core block loop: batches of at most kDmaMaxBatch -------------------------------
 // The vector-unit loops spend ~100 G instructions per block pair and lane on q . k and
 // P V, which bounds large groups below the memory rate (Qwen2.5-VL, G = 7: 68.6 us here
 // against 59.7) and costs the Qwen3-8B batch (G = 4) 2%.  Here, per block of 16 keys:
