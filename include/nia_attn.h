@@ -245,7 +245,7 @@ int32_t nia_qk_norm_rope_kv_write_fp8(void* q, int64_t q_tok_stride, int64_t q_h
 /*
  * Paged decode over fp8 caches: nia_paged_decode with k_cache / v_cache in the fp8
  * format above (uint8 codes, k_scale / v_scale fp32 [num_blocks, num_kv_heads,
- * block_size]).  q and out are bf16; keys are dequantised exactly as
+ * block_size], 16-byte aligned, else NIA_ERR_MISALIGNED).  q and out are bf16; keys are dequantised exactly as
  * code * row scale (the code is widened to bf16 without rounding, the scale
  * multiplies the q . k score, and each softmax weight carries its row's v scale).
  * Same workspace contract and shapes as nia_paged_decode (head_dim 128, block

@@ -1562,7 +1562,8 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
   if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
       q_batch_stride % vec || q_head_stride % vec)
     return NIA_ERR_MISALIGNED;
-  if (fp8 && ((uintptr_t)k_scale % 4 || (uintptr_t)v_scale % 4)) return NIA_ERR_MISALIGNED;
+  // the matrix-core loop reads a block-head's row scales four at a time (16 bytes)
+  if (fp8 && ((uintptr_t)k_scale % 16 || (uintptr_t)v_scale % 16)) return NIA_ERR_MISALIGNED;
 
   DecodeParams p;
   p.out = out;

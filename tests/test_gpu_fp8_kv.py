@@ -164,6 +164,20 @@ def test_decode_fp8_at_the_staged_batch_limit(heads, batch):
                       f"fp8 G={heads // 4} batch {batch}")
 
 
+def test_decode_fp8_rejects_scales_off_a_16_byte_boundary():
+    """The decode reads a block-head's row scales 16 bytes at a time: a scale tensor that
+    starts 4 bytes into an allocation is refused before any launch."""
+    c = workloads.make_decode(2, 8, 2, 128, [40, 70], 16, 16, torch.bfloat16, "cuda", seed=3)
+    f8 = workloads.quantize_cache_fp8(c)
+    ks = f8.k_scale[0]
+    shifted = torch.empty(ks.numel() + 1, dtype=torch.float32, device="cuda")[1:].view(ks.shape)
+    shifted.copy_(ks)
+    with pytest.raises(RuntimeError, match="(?i)align"):
+        ops.paged_decode(c.q, f8.k_cache[0], f8.v_cache[0], c.block_tables, c.context_lens,
+                         k_scale=shifted, v_scale=f8.v_scale[0])
+    torch.cuda.synchronize()
+
+
 def test_decode_fp8_qwen3_8b_sampled_rows():
     """The 64-sequence Qwen3-8B workload; every row checked on 12 sequences."""
     c = workloads.decode_qwen3_8b("cuda")
