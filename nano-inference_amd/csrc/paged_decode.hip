@@ -32,8 +32,8 @@
 //   bf16 pair and moved from the K lanes to the V lanes with ds_bpermute.
 // fp32 (same shapes)
 //   paged_decode_partial_kernel: grid (partition, KV head, sequence); wave w takes
-//   blocks w, w + 4, ... of the partition; 16 lanes per token in one layout for
-//   both K and V.
+//   blocks w, w + 4, ... of the partition; 32 lanes per token in one layout for
+//   both K and V; q . k is summed in fp64.
 // Softmax (both)
 //   Scores are kept in log2 units (scale * log2 e folded in).  Each lane row keeps
 //   its own running (l, o[8 dims]) against a running max (per lane row in fp32, one
@@ -139,11 +139,28 @@ struct Elem<float> {
     s = fmaf(q.f[2], as_f32(k.z), s);
     return fmaf(q.f[3], as_f32(k.w), s);
   }
+  // The lane's share of q . k in fp64: the fp32 path's scores carry no accumulated
+  // rounding (an fp32 sum of 128 products is off by ~1e-7 of the largest partial sum,
+  // which at logits of ~100 nats moves the softmax weights by ~1e-5).
+  static NIA_DEVICE double dot64(const QReg& q, const uint4& k) {
+    double s = (double)q.f[0] * (double)as_f32(k.x);
+    s = fma((double)q.f[1], (double)as_f32(k.y), s);
+    s = fma((double)q.f[2], (double)as_f32(k.z), s);
+    return fma((double)q.f[3], (double)as_f32(k.w), s);
+  }
   static NIA_DEVICE void widen(const uint4& v, float (&f)[4]) {
     f[0] = as_f32(v.x); f[1] = as_f32(v.y); f[2] = as_f32(v.z); f[3] = as_f32(v.w);
   }
   static NIA_DEVICE float from_f32(float x) { return x; }
 };
+
+// Sum of doubles over aligned groups of N lanes (N a power of two, at most 64).
+template <int N>
+NIA_DEVICE double group_sum_f64(double x) {
+#pragma unroll
+  for (int off = 1; off < N; off <<= 1) x += __shfl_xor(x, off, kWave);
+  return x;
+}
 
 // Merge the per-wave softmax states of a workgroup held in LDS and store either the
 // final output (single-partition sequence) or the partition's partial (m, l,
@@ -295,8 +312,12 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_partial_kernel(De
       const bool valid = full || (jb * BS + i * TPL + row) < ctx;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float s = group_sum<LPT>(E::dot(qr[g], buf.k[i]));
-        x[i][g] = valid ? s * p.scale_log2 : -INFINITY;
+        float s;
+        if constexpr (std::is_same<T, float>::value)
+          s = (float)(group_sum_f64<LPT>(E::dot64(qr[g], buf.k[i])) * (double)p.scale_log2);
+        else
+          s = group_sum<LPT>(E::dot(qr[g], buf.k[i])) * p.scale_log2;
+        x[i][g] = valid ? s : -INFINITY;
       }
     }
     bool need = false;
@@ -892,7 +913,7 @@ NIA_DEVICE void decode_item(const DecodeParams& p, int b, int hk, int part, int 
 // P V, which bounds large groups below the memory rate (Qwen2.5-VL, G = 7: 68.6 us here
 // against 59.7) and costs the Qwen3-8B batch (G = 4) 2%.  Here, per block of 16 keys:
 //   S^T = K Q^T: 4 v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims of K, B = Q^T with the
-//         group's heads in columns 0..G-1 and zeros beyond, scaled by scale * log2 e);
+//         group's heads in columns 0..G-1 and zeros beyond), then scale * log2 e in fp32;
 //   O^T += V^T P^T: 8 v_mfma_f32_16x16x16_bf16, one per 16-dim tile (A = V^T read from
 //         LDS with ds_read_b64_tr_b16, B = P^T, which is the S^T accumulator as it is).
 // In both accumulators lane l owns head l % 16 and rows 4 (l / 16) .. + 3 of the tile, so
@@ -996,7 +1017,9 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
   const int my_bt = (lane < blk_end - blk_begin) ? bt[blk_begin + lane] : -1;
 
   // B operand of S^T: head hn, dims 32 j + 8 quad .. + 7 (fp8: 64 (j / 2) + 16 quad + 8 (j % 2)
-  // .. + 7, the order of the K codes), times scale * log2(e) (bf16)
+  // .. + 7, the order of the K codes), as given: the scores leave the MFMAs as exact-product
+  // fp32 sums and take scale * log2(e) in fp32 (a bf16-rounded scaled Q would move each
+  // score by up to 2^-9 of its size)
   uint4 qb[4];
   {
     const bf16_t* qp = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)b * p.q_b +
@@ -1004,12 +1027,7 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int d0 = FP8 ? 64 * (j >> 1) + 16 * quad + 8 * (j & 1) : 32 * j + 8 * quad;
-      const uint4 u = hn < G ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
-      uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf16x2(bf16_lo(w[e]) * p.scale_log2, bf16_hi(w[e]) * p.scale_log2);
-      qb[j] = make_uint4(w[0], w[1], w[2], w[3]);
+      qb[j] = hn < G ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
     }
   }
   f32x4_t oacc[8];
@@ -1101,10 +1119,13 @@ NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part,
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         if constexpr (FP8) {
-          sc[x][0] *= ksc[x].x;
-          sc[x][1] *= ksc[x].y;
-          sc[x][2] *= ksc[x].z;
-          sc[x][3] *= ksc[x].w;
+          sc[x][0] *= ksc[x].x * p.scale_log2;
+          sc[x][1] *= ksc[x].y * p.scale_log2;
+          sc[x][2] *= ksc[x].z * p.scale_log2;
+          sc[x][3] *= ksc[x].w * p.scale_log2;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[x][i] *= p.scale_log2;
         }
         const bool ok = x ? bB >= 0 : bA >= 0;
 #pragma unroll
@@ -1635,3 +1656,4 @@ extern "C" int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride,
                             num_heads, num_kv_heads, head_dim, block_size, num_blocks, scale,
                             workspace, workspace_bytes, NIA_DTYPE_BF16, stream);
 }
+

@@ -28,13 +28,13 @@
 //   XOR-swizzled per row (prefill_kernel).  Every O^T register of a
 //   lane belongs to that lane's query, so rescaling O is lane-local.
 // Softmax: exp2 of scores in log2 units; the running max is only raised when a tile
-// could hold a P above 2^8 (lazy rescale).  prefill_kernel folds scale * log2(e) and
-// the max into one FMA per score and tests the tile's row max.  prefill_dma_kernel
-// scales Q by scale * log2(e) once (rounded to bf16) and starts each tile's QK chain
-// with the accumulator at minus the running max, so the MFMAs hand over scores that
-// exp2 takes as they are; it computes P against the running max first and reduces
-// the row max only when a lane's sum of the tile's P exceeds 2^8 (or the row has no
-// max yet), which keeps the max reduction off the vector unit's common path.
+// could hold a P above 2^8 (lazy rescale).  Both kernels take the raw scores q . k
+// from the MFMAs in fp32 and fold scale * log2(e) and the max into one FMA per score
+// (Q stays as given: scaling it in bf16 would round each score by up to 2^-9 of its
+// size).  prefill_kernel tests the tile's row max; prefill_dma_kernel computes P
+// against the running max first and reduces the row max only when a lane's sum of the
+// tile's P exceeds 2^8 (or the row has no max yet), which keeps the max reduction off
+// the vector unit's common path.
 // Causal tiles above the diagonal are never visited; tiles crossing it are masked.
 // MFMA work per (query, key) pair: 4 * D flops (QK^T and PV).
 #include <type_traits>
@@ -541,19 +541,6 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       qreg[kk] = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * kk + 8 * half)
                         : make_uint4(0, 0, 0, 0);
   }
-  // Scores in log2 units straight from the MFMAs: q * scale * log2(e), rounded to bf16
-  // (not for paired heads).  Called once the first K/V tile's DMA is out, so that Q's
-  // load latency overlaps it.
-  auto scale_q = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int kk = 0; kk < DK; ++kk) {
-      uint32_t w[4] = {qreg[kk].x, qreg[kk].y, qreg[kk].z, qreg[kk].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        w[j] = pack_bf16x2(bf16_lo(w[j]) * p.scale_log2, bf16_hi(w[j]) * p.scale_log2);
-      qreg[kk] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  };
   f32x16_t oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -561,11 +548,6 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
   float m_run = -INFINITY;
   float l_run = 0.f;
-  // Initial accumulator of every QK chain: minus the running max (0 before the row has
-  // one), so a tile's scores arrive relative to it.
-  f32x16_t sinit;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) sinit[r] = 0.f;
 
   // ---- DMA geometry: instruction i of wave w writes rows 16w + 4i + (lane / 16) ----------
   const int ld_sub = lane >> 4;
@@ -675,10 +657,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kTileRowBytes + k_off[kk]);
-        // paired heads: scores are absolute, the chain starts from zero
+        // raw scores q . k in fp32 (the bf16 products are exact)
         sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]),
-            kk == 0 ? (PAIR ? f32x16_t{} : sinit) : sacc[c], 0, 0, 0);
+            kk == 0 ? f32x16_t{} : sacc[c], 0, 0, 0);
       }
     }
     // Issue order: K operand reads run six MFMAs ahead.
@@ -698,16 +680,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         for (int r = 0; r < 16; ++r)
           if (32 * c + 8 * (r >> 2) + (r & 3) >= lim) sacc[c][r] = -INFINITY;
     }
-    // P against the running max (the scores already are relative to it).  The tile's
-    // max is only computed (slow path) when the row has no max yet or a lane's sum of
-    // this tile's P exceeds 2^8: every P is at most its lane's sum, so below that bound
-    // no P exceeds 2^8 and the max may stay.
+    // P against the running max: p = exp2(s * scale * log2(e) - m), one FMA per score in
+    // fp32 (scaling Q in bf16 instead would round every score by up to 2^-9 of its size,
+    // which at logits of tens of nats moves the weights by percents).  The tile's max is
+    // only computed (slow path) when the row has no max yet or a lane's sum of this
+    // tile's P exceeds 2^8: every P is at most its lane's sum, so below that bound no P
+    // exceeds 2^8 and the max may stay.
     uint4 pb[4];
     float lt = 0.f;  // this lane's sum of the tile's P (bf16, as the P V product uses them)
-    // Paired heads (windows of one tile, which always take the slow path) keep Q unscaled
-    // and fold scale * log2(e) and the max into one FMA per score, as scaling Q would
-    // only add to their short critical path.
-    auto exps = [&](auto shifted, float shift) __attribute__((always_inline)) {
+    auto exps = [&](float shift) __attribute__((always_inline)) {
       lt = 0.f;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -716,14 +697,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
           uint32_t w[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            float x0 = sacc[c][8 * hh + 2 * j], x1 = sacc[c][8 * hh + 2 * j + 1];
-            if constexpr (PAIR) {
-              x0 = fmaf(x0, p.scale_log2, shift);
-              x1 = fmaf(x1, p.scale_log2, shift);
-            } else if constexpr (decltype(shifted)::value) {
-              x0 += shift;
-              x1 += shift;
-            }
+            const float x0 = fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, shift);
+            const float x1 = fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, shift);
             w[j] = pack_bf16x2(fast_exp2(x0), fast_exp2(x1));
             lt = dot2_bf16(w[j], kBf16OnePair, lt);
           }
@@ -733,7 +708,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     };
     bool slow = wave_any(m_run == -INFINITY);
     if (!slow) {
-      exps(std::false_type(), PAIR ? -m_run : 0.f);  // m_run is finite here
+      exps(-m_run);  // m_run is finite here
       slow = wave_any(lt > kLazyRescaleBound);
     }
     if (slow) {
@@ -742,11 +717,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
-      // the scores are relative to msub (unscaled absolute ones for paired heads); the
-      // new max and its offset are absolute
-      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
-      const float mn =
-          fmaxf(m_run, PAIR ? max_xor32(mx) * p.scale_log2 : msub + max_xor32(mx));
+      const float mn = fmaxf(m_run, max_xor32(mx) * p.scale_log2);
       const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
       m_run = mn;
       const float msub_new = (mn == -INFINITY) ? 0.f : mn;
@@ -755,11 +726,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
-      exps(std::true_type(), PAIR ? -msub_new : msub - msub_new);
-      if constexpr (!PAIR) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sinit[r] = -msub_new;
-      }
+      exps(-msub_new);
     }
     l_run += lt;
 #pragma unroll
@@ -804,7 +771,6 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   // Unrolled by two so that each stage's LDS offsets are compile-time constants.
     int blk_nxt = block_of(0);
     issue_tile(0, 0, blk_nxt);
-    scale_q();
     if (kBlockN < n_end) blk_nxt = block_of(kBlockN);
     auto step = [&](int n0, auto stage_c) __attribute__((always_inline)) {
       constexpr int kStage = decltype(stage_c)::value;

@@ -1,0 +1,254 @@
+"""Logits of tens of nats: the lazy-rescale branches of every kernel vs the oracle.
+
+With N(0, 1) inputs a later block or tile never exceeds a row's running max by the
+2^8 that triggers a rescale, so the raise-max / rescale-O / recompute-P paths are
+otherwise untested.  Here queries and keys share a direction (tests/logit_inputs.py)
+so that logits reach ~100 nats:
+  ramp   every later block / tile raises the max by more than 2^8;
+  late   two dominant keys, one a third into the context and one at its end;
+  fall   the first key dominates and the rest underflow;
+  scaled q and k times 4 (logits ~N(0, 16^2)).
+Kernels: decode on the matrix-core loop (batch <= 1024) for groups of 1, 4 and 7, on
+the vector loops (batch 1025), in fp32 and over fp8 caches; causal, chunked, vision
+full (D 80), paired-head windows and paired heads over many key tiles.
+Oracle: oracle.textbook in float64 (softmax(q K^T / sqrt(D)) V, the mathematics of
+src/nano_inference/layers/attention.py:12-50 and :285-332).
+Bars: bf16 max-abs 2e-2 / mean-abs 2e-3; fp32 max-abs 1e-5.  Each test prints its
+largest logit and its errors.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nano_inference_amd import ops, workloads
+from oracle import fp8_kv as F
+from oracle import textbook as tb
+from tests import logit_inputs as LI
+from tests.tolerances import assert_attn_close, errors
+
+pytestmark = pytest.mark.gpu
+
+MODES = ["ramp", "late", "fall", "scaled"]
+
+
+def _report(what, out, ref, logit):
+    mx, mean = errors(out, ref)
+    print(f"LOGITS {what}: max logit {logit:.1f} nats, max-abs {mx:.3g}, mean-abs {mean:.3g}",
+          flush=True)
+
+
+def _decode_oracle(c, seqs, dequant=None):
+    """Float64 decode oracle over the case's cache (or its dequantised fp8 rows),
+    plus the largest |logit| seen."""
+    b, h, d = c.q.shape
+    hkv = c.num_kv_heads
+    g = h // hkv
+    q = c.q.double().cpu().numpy()
+    out = np.zeros((len(seqs), h, d))
+    scale = 1.0 / math.sqrt(d)
+    top = 0.0
+    for n, i in enumerate(seqs):
+        L = c.lens[i]
+        ids = torch.tensor(c.tables_list[i], device=c.k_cache.device)
+        if dequant is None:
+            kb = c.k_cache[0][ids].double().cpu().numpy()
+            vb = c.v_cache[0][ids].double().cpu().numpy()
+        else:
+            kb, vb = dequant(ids)
+        kk = kb.transpose(1, 0, 2, 3).reshape(hkv, -1, d)[:, :L]
+        vv = vb.transpose(1, 0, 2, 3).reshape(hkv, -1, d)[:, :L]
+        for hk in range(hkv):
+            qq = q[i, hk * g:(hk + 1) * g]
+            out[n, hk * g:(hk + 1) * g] = tb.attend(qq, kk[hk], vv[hk], scale)
+            if L:
+                top = max(top, float(np.abs(qq @ kk[hk].T).max() * scale))
+    return out, top
+
+
+def _step(c):
+    ops.kv_write(c.k_new, c.v_new, c.k_cache[0], c.v_cache[0], c.slot_mapping)
+    out = ops.paged_decode(c.q, c.k_cache[0], c.v_cache[0], c.block_tables, c.context_lens)
+    torch.cuda.synchronize()
+    return out
+
+
+DECODE_LENS = [1, 2, 17, 300, 777, 2048, 4100]
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("group", [1, 4, 7])
+def test_decode_matrix_core_loop(group, mode):
+    c = workloads.make_decode(len(DECODE_LENS), 4 * group, 4, 128, DECODE_LENS, 2048, 16,
+                              torch.bfloat16, "cuda", seed=700 + group)
+    LI.shape_decode(c, mode, seed=group)
+    out = _step(c)
+    seqs = list(range(len(DECODE_LENS)))
+    ref, top = _decode_oracle(c, seqs)
+    _report(f"decode bf16 G={group} {mode}", out, ref, top)
+    assert_attn_close(out, ref, torch.bfloat16, f"decode G={group} {mode}")
+
+
+@pytest.mark.parametrize("mode", ["ramp", "late"])
+@pytest.mark.parametrize("group", [4, 7])
+def test_decode_vector_loops(group, mode):
+    """1025 sequences (above the matrix-core loop's batch limit); most are short, the
+    checked ones carry long shaped contexts."""
+    g = torch.Generator().manual_seed(901 + group)
+    lens = [int(x) for x in torch.randint(1, 41, (1025,), generator=g)]
+    checked = [3, 100, 517, 1000, 1024]
+    for n, i in enumerate(checked):
+        lens[i] = [300, 700, 1200, 2000, 333][n]
+    c = workloads.make_decode(1025, 4 * group, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",
+                              seed=910 + group, max_blocks=128)
+    LI.shape_decode(c, mode, seed=group + 10)
+    out = _step(c)
+    ref, top = _decode_oracle(c, checked)
+    _report(f"decode bf16 batch 1025 G={group} {mode}", out[checked], ref, top)
+    assert_attn_close(out[checked], ref, torch.bfloat16, f"decode 1025 G={group} {mode}")
+
+
+@pytest.mark.parametrize("mode", ["ramp", "late", "fall"])
+@pytest.mark.parametrize("group", [2, 4])
+def test_decode_fp32(group, mode):
+    c = workloads.make_decode(len(DECODE_LENS), 4 * group, 4, 128, DECODE_LENS, 2048, 16,
+                              torch.float32, "cuda", seed=720 + group)
+    LI.shape_decode(c, mode, seed=group + 20)
+    out = _step(c)
+    ref, top = _decode_oracle(c, list(range(len(DECODE_LENS))))
+    _report(f"decode fp32 G={group} {mode}", out, ref, top)
+    assert_attn_close(out, ref, torch.float32, f"decode fp32 G={group} {mode}")
+
+
+@pytest.mark.parametrize("mode", ["ramp", "late"])
+@pytest.mark.parametrize("group", [4, 7])
+def test_decode_fp8_cache(group, mode):
+    c = workloads.make_decode(len(DECODE_LENS), 4 * group, 4, 128, DECODE_LENS, 2048, 16,
+                              torch.bfloat16, "cuda", seed=740 + group)
+    LI.shape_decode(c, mode, seed=group + 30)
+    ops.kv_write(c.k_new, c.v_new, c.k_cache[0], c.v_cache[0], c.slot_mapping)
+    f8 = workloads.quantize_cache_fp8(c)
+    out = ops.paged_decode(c.q, f8.k_cache[0], f8.v_cache[0], c.block_tables, c.context_lens,
+                           k_scale=f8.k_scale[0], v_scale=f8.v_scale[0])
+    torch.cuda.synchronize()
+
+    def dequant(ids):
+        kb = F.dequantize_rows(f8.k_cache[0][ids].cpu(), f8.k_scale[0][ids].cpu())
+        vb = F.dequantize_rows(f8.v_cache[0][ids].cpu(), f8.v_scale[0][ids].cpu())
+        return kb.double().numpy(), vb.double().numpy()
+
+    ref, top = _decode_oracle(c, list(range(len(DECODE_LENS))), dequant)
+    _report(f"decode fp8 G={group} {mode}", out, ref, top)
+    assert_attn_close(out, ref, torch.bfloat16, f"decode fp8 G={group} {mode}")
+
+
+def _varlen_check(out, q, k, v, qs, ql, ks, kl, mode_mask, what, dtype=torch.bfloat16):
+    qn, kn, vn = (t.double().cpu().numpy() for t in (q, k, v))
+    d = qn.shape[2]
+    scale = 1.0 / math.sqrt(d)
+    res = tb.varlen(qn, kn, vn, qs, ql, ks, kl, scale, mode_mask)
+    o = out.double().cpu().numpy()
+    got = np.concatenate([o[int(qs[s]) + idx] for s, (idx, _) in res.items()])
+    exp = np.concatenate([r for _, (_, r) in res.items()])
+    g = qn.shape[1] // kn.shape[1]
+    top = 0.0
+    for s in range(len(qs)):
+        if ql[s] and kl[s]:
+            for hh in (0, qn.shape[1] - 1):
+                a = qn[qs[s]:qs[s] + ql[s], hh] @ kn[ks[s]:ks[s] + kl[s], hh // g].T
+                top = max(top, float(np.abs(a).max() * scale))
+    _report(what, got, exp, top)
+    assert_attn_close(got, exp, dtype, what)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_causal_prefill(mode):
+    lens = [1, 63, 64, 65, 129, 300, 1000]
+    c = workloads.make_varlen(lens, 8, 2, 128, torch.bfloat16, "cuda", seed=760, causal=True)
+    cu = c.cu_seqlens.tolist()
+    LI.shape_rows(c.q, c.k, cu[:-1], lens, cu[:-1], lens, mode, seed=61)
+    out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=True)
+    torch.cuda.synchronize()
+    _varlen_check(out, c.q, c.k, c.v, cu[:-1], lens, cu[:-1], lens, "top_left",
+                  f"causal prefill {mode}")
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_chunked_prefill(mode):
+    c = workloads.chunked_qwen3_8b("cuda", n=4, chunk=200, prior=[0, 100, 700, 1500],
+                                   num_heads=8, num_kv_heads=2, seed=3200)
+    LI.shape_chunked(c, mode, seed=62)
+    out = ops.prefill_paged(c.q, c.k_cache, c.v_cache, c.block_tables, c.q_start, c.q_len,
+                            c.context_lens, c.chunk)
+    torch.cuda.synchronize()
+    q = c.q.double().cpu().numpy()
+    o = out.double().cpu().numpy()
+    hkv, g = 2, 4
+    got, exp, top = [], [], 0.0
+    for s in range(4):
+        L = c.prior[s] + c.chunk
+        ids = torch.tensor(c.tables_list[s], device="cuda")
+        kk = c.k_cache[ids].double().cpu().numpy().transpose(1, 0, 2, 3).reshape(hkv, -1, 128)[:, :L]
+        vv = c.v_cache[ids].double().cpu().numpy().transpose(1, 0, 2, 3).reshape(hkv, -1, 128)[:, :L]
+        bnd = tb.causal_bounds(c.chunk, L, "bottom_right")
+        r = np.zeros((c.chunk, 8, 128))
+        for hh in range(8):
+            qq = q[s * c.chunk:(s + 1) * c.chunk, hh]
+            r[:, hh] = tb.attend(qq, kk[hh // g], vv[hh // g], 1 / math.sqrt(128), bnd)
+            top = max(top, float(np.abs(qq @ kk[hh // g].T).max() / math.sqrt(128)))
+        got.append(o[s * c.chunk:(s + 1) * c.chunk])
+        exp.append(r)
+    got, exp = np.concatenate(got), np.concatenate(exp)
+    _report(f"chunked prefill {mode}", got, exp, top)
+    assert_attn_close(got, exp, torch.bfloat16, f"chunked prefill {mode}")
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_vision_full_d80(mode):
+    lens = [784, 300, 65]
+    c = workloads.make_varlen(lens, 4, 4, 80, torch.bfloat16, "cuda", seed=780, causal=False)
+    cu = c.cu_seqlens.tolist()
+    LI.shape_rows(c.q, c.k, cu[:-1], lens, cu[:-1], lens, mode, seed=63)
+    out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=False)
+    torch.cuda.synchronize()
+    _varlen_check(out, c.q, c.k, c.v, cu[:-1], lens, cu[:-1], lens, "none",
+                  f"vision full {mode}")
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_paired_head_windows(mode):
+    lens = [64, 33, 8, 64, 17, 1, 50]
+    c = workloads.make_varlen(lens, 6, 6, 80, torch.bfloat16, "cuda", seed=790, causal=False)
+    cu = c.cu_seqlens.tolist()
+    LI.shape_rows(c.q, c.k, cu[:-1], lens, cu[:-1], lens, mode, seed=64)
+    out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=False)
+    torch.cuda.synchronize()
+    _varlen_check(out, c.q, c.k, c.v, cu[:-1], lens, cu[:-1], lens, "none",
+                  f"paired windows {mode}")
+
+
+@pytest.mark.parametrize("mode", [None, "ramp", "late", "scaled"])
+@pytest.mark.parametrize("head_dim", [64, 80, 128])
+def test_paired_heads_over_many_key_tiles(head_dim, mode):
+    """Unmasked calls with at most 64 queries and H == H_kv take the paired-head kernel
+    whatever the key count: queries 1..64 over 65..700 keys (several key tiles), every
+    row checked, with N(0, 1) inputs (mode None) and with large logits."""
+    g = torch.Generator().manual_seed(800 + head_dim)
+    ql = [1, 5, 64, 33, 64, 17]
+    kl = [65, 700, 129, 64 * 5 + 3, 511, 200]
+    h = 4
+    tq, tk = sum(ql), sum(kl)
+    q = torch.randn(tq, h, head_dim, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(tk, h, head_dim, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(tk, h, head_dim, generator=g).to(torch.bfloat16).cuda()
+    qs = [0] + list(np.cumsum(ql)[:-1])
+    ks = [0] + list(np.cumsum(kl)[:-1])
+    if mode is not None:
+        LI.shape_rows(q, k, qs, ql, ks, kl, mode, seed=65 + head_dim)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    out = ops.prefill(q, k, v, torch.tensor(qs, **i32), torch.tensor(ql, **i32),
+                      torch.tensor(ks, **i32), torch.tensor(kl, **i32), max(ql),
+                      ops.CAUSAL_NONE)
+    torch.cuda.synchronize()
+    _varlen_check(out, q, k, v, qs, ql, ks, kl, "none", f"paired multi-tile D={head_dim} {mode}")

@@ -1,0 +1,346 @@
+"""Decoder layers at the served models' shapes, and whole-model generation, against the
+reference pipeline restated in float64 on the CPU.
+
+* A packed step (PackedAttentionMetadata: decode rows and prefill-chunk rows in one
+  row of tokens) through PagedCausalSelfAttention at the Qwen3-0.6B layer shape
+  (hidden 1024, 16/8 heads, D 128, QK-RMSNorm, RoPE theta 1e6), over bf16 and fp8
+  caches.  CPU side: projections, QK-norm and RoPE as the reference's ops
+  (oracle.qk_rope), the write loop (oracle.reference_attention.kv_write_loop,
+  src/nano_inference/layers/attention.py:267-278), then per sequence the float64
+  textbook attention over keys [0, context_len) with a bottom-right causal bound
+  for chunk rows (a decode row sees its whole context, as :285-332).
+* Qwen25VLDecoderAttention at the Qwen2.5-VL decoder shape (28/4 heads, D 128,
+  qkv_bias, mRoPE sections (16, 24, 24)): an image-and-text prefill with explicit
+  (3, B, S) positions, then decode steps (src/nano_inference/layers/attention.py:
+  343-371 and :220-340); metadata from the oracle's restated context builder.
+* Teacher forcing on a 2-layer Qwen3-0.6B-architecture model (full vocabulary):
+  every greedy token of both generators must be a maximum of the float64 CPU
+  recompute's logits at its position, up to bf16 noise.
+Module-level bar (bf16 activations between every op on the GPU side):
+max-abs <= 3e-2, mean-abs <= 3e-3.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as Fn
+
+from nano_inference_amd import (AttentionMetadata, PagedCausalSelfAttention,
+                                Qwen25VLDecoderAttention, e2e, ops)
+from nano_inference_amd.context import PackedAttentionMetadata
+from oracle import fp8_kv as F8
+from oracle import metadata as meta
+from oracle import qk_rope as O
+from oracle import reference_attention as ref
+from oracle import textbook as tb
+
+pytestmark = pytest.mark.gpu
+
+MOD_MAX_ABS = 3e-2
+MOD_MEAN_ABS = 3e-3
+
+
+def close(out, exp, what):
+    d = (out.double().cpu() - exp.double().cpu()).abs()
+    assert torch.isfinite(out).all(), what
+    print(f"LAYER {what}: max-abs {d.max().item():.3g}, mean-abs {d.mean().item():.3g}",
+          flush=True)
+    assert d.max().item() <= MOD_MAX_ABS and d.mean().item() <= MOD_MEAN_ABS, (
+        f"{what}: max-abs {d.max().item():.3g}, mean-abs {d.mean().item():.3g}")
+
+
+def cpu_qkv(m, x, pos, mrope=False):
+    """Projections, QK-norm and (m)RoPE of module ``m`` in float64 on the CPU.
+    x (..., S, hidden) -> q (..., S, H, D), k, v (..., S, H_kv, D)."""
+    sd = {k: v.detach().double().cpu() for k, v in m.state_dict().items()}
+    lead = x.shape[:-1]
+
+    def lin(name):
+        y = x @ sd[name + ".weight"].T
+        return y + sd[name + ".bias"] if name + ".bias" in sd else y
+
+    q = lin("q_proj").view(*lead, m.num_heads, m.head_dim)
+    k = lin("k_proj").view(*lead, m.num_kv_heads, m.head_dim)
+    v = lin("v_proj").view(*lead, m.num_kv_heads, m.head_dim)
+    eps = m.q_norm.eps if m.q_norm is not None else 0.0
+    qw = sd.get("q_norm.weight")
+    kw = sd.get("k_norm.weight")
+    inv = m.rotary.inv_freq.detach().float().cpu()
+    section = m.rotary._section_freqs if mrope else None
+    q, k = O.qk_norm_rope(q, k, qw, kw, eps, pos, inv, section)
+    return q, k, v, sd
+
+
+def cpu_paged_rows(q, kc, vc, tables, ctx, q_start, q_len):
+    """Float64 attention of packed rows q (T, H, D): sequence s's rows attend its keys
+    [0, ctx[s]) in the paged caches with the bottom-right causal bound."""
+    hkv = kc.shape[1]
+    h = q.shape[1]
+    g = h // hkv
+    out = torch.zeros_like(q)
+    qn = q.numpy()
+    for s in range(len(ctx)):
+        L, qs, ql = int(ctx[s]), int(q_start[s]), int(q_len[s])
+        bnd = tb.causal_bounds(ql, L, "bottom_right")
+        for hk in range(hkv):
+            kk = tb.gather_paged(kc.numpy(), np.asarray(tables[s]), L, hk)
+            vv = tb.gather_paged(vc.numpy(), np.asarray(tables[s]), L, hk)
+            for hh in range(hk * g, (hk + 1) * g):
+                out[qs:qs + ql, hh] = torch.from_numpy(
+                    tb.attend(qn[qs:qs + ql, hh], kk, vv, 1 / math.sqrt(q.shape[2]), bnd))
+    return out
+
+
+class PackedStepper:
+    """Runs packed steps through the GPU layer and the float64 CPU pipeline side by side."""
+
+    def __init__(self, m, nb, bs, fp8):
+        self.m, self.bs, self.fp8 = m, bs, fp8
+        hkv, d = m.num_kv_heads, m.head_dim
+        cdt = torch.uint8 if fp8 else torch.bfloat16
+        self.kc = torch.zeros((1, nb, hkv, bs, d), dtype=cdt, device="cuda")
+        self.vc = torch.zeros_like(self.kc)
+        self.ks = self.vs = None
+        if fp8:
+            self.ks = torch.zeros((1, nb, hkv, bs), dtype=torch.float32, device="cuda")
+            self.vs = torch.zeros_like(self.ks)
+        self.kc_cpu = torch.zeros((nb, hkv, bs, d), dtype=torch.float64)
+        self.vc_cpu = torch.zeros_like(self.kc_cpu)
+
+    def step(self, entries, tables, hidden_seed):
+        """entries: (start, n, decode) per sequence, decodes first."""
+        bs = self.bs
+        nd = sum(1 for e in entries if e[2])
+        q_start, q_len, ctx, slots, pos = [], [], [], [], []
+        row = 0
+        for (start, n, _), tb_ in zip(entries, tables):
+            q_start.append(row)
+            q_len.append(n)
+            ctx.append(start + n)
+            for j in range(n):
+                p = start + j
+                pos.append(p)
+                slots.append(tb_[p // bs] * bs + p % bs)
+            row += n
+        t = row
+        g = torch.Generator().manual_seed(hidden_seed)
+        x = (torch.randn(1, t, self.m.hidden_size, generator=g) * 0.5).to(torch.bfloat16)
+        width = max(len(x_) for x_ in tables)
+        bt = torch.zeros((len(tables), width), dtype=torch.int32)
+        for i, x_ in enumerate(tables):
+            bt[i, :len(x_)] = torch.tensor(x_, dtype=torch.int32)
+        i32 = dict(dtype=torch.int32, device="cuda")
+        md = PackedAttentionMetadata(
+            context_lens=torch.tensor(ctx, dtype=torch.int64, device="cuda"),
+            kv_block_tables=bt.cuda(),
+            slot_mapping=torch.tensor(slots, dtype=torch.int64, device="cuda").view(1, t),
+            k_cache=self.kc, v_cache=self.vc, k_scale=self.ks, v_scale=self.vs,
+            is_prefill=nd < len(entries), q_start=torch.tensor(q_start, **i32),
+            q_len=torch.tensor(q_len, **i32), num_decode=nd,
+            max_q_len=max([e[1] for e in entries[nd:]], default=1))
+        posg = torch.tensor(pos, dtype=torch.int64).view(1, t)
+        with torch.no_grad():
+            out = self.m(x.cuda(), posg.cuda(), None, md)
+        torch.cuda.synchronize()
+        # CPU: same step in float64; the cache takes the CPU's own k/v rows (for fp8, the
+        # rows the GPU quantised are dequantised instead, as the format is the cache)
+        q, k, v, sd = cpu_qkv(self.m, x.double(), posg)
+        if self.fp8:
+            ids = torch.tensor(slots) // bs
+            sl = torch.tensor(slots) % bs
+            kq = F8.dequantize_rows(self.kc[0].cpu(), self.ks[0].cpu()).double()
+            vq = F8.dequantize_rows(self.vc[0].cpu(), self.vs[0].cpu()).double()
+            self.kc_cpu[ids, :, sl] = kq[ids, :, sl]
+            self.vc_cpu[ids, :, sl] = vq[ids, :, sl]
+        else:
+            ref.kv_write_loop(k, v, self.kc_cpu, self.vc_cpu, torch.tensor(slots).view(1, t))
+        a = cpu_paged_rows(q[0], self.kc_cpu, self.vc_cpu, tables, ctx, q_start, q_len)
+        exp = a.reshape(1, t, -1) @ sd["o_proj.weight"].T
+        return out, exp
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_packed_step_qwen3_0p6b_layer(fp8):
+    torch.manual_seed(10)
+    m = PagedCausalSelfAttention(1024, 16, num_kv_heads=8, head_dim=128, use_qk_norm=True,
+                                 rope_base=1e6).to("cuda", torch.bfloat16).eval()
+    with torch.no_grad():  # QK-norm weights away from one, as a trained model's
+        m.q_norm.weight.copy_(1 + 0.3 * torch.randn(128))
+        m.k_norm.weight.copy_(1 + 0.3 * torch.randn(128))
+    m.layer_idx = 0
+    bs, nb = 16, 256
+    st = PackedStepper(m, nb, bs, fp8)
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(11)).tolist()
+    prompts = [40, 300, 17, 150, 90, 260]
+    tables, off = [], 0
+    for L in prompts:
+        n = -(-(L + 8) // bs)
+        tables.append(perm[off:off + n])
+        off += n
+    # step 1: the first three prompts whole, the others' first chunks (prefill only)
+    e1 = [(0, 40, False), (0, 300, False), (0, 17, False), (0, 64, False), (0, 1, False),
+          (0, 100, False)]
+    out, exp = st.step(e1, tables, 1)
+    close(out, exp, f"packed prefill chunks fp8={fp8}")
+    # step 2: three decodes plus the others' next chunks, ending prompt 4 and 5
+    e2 = [(40, 1, True), (300, 1, True), (17, 1, True), (64, 86, False), (1, 89, False),
+          (100, 60, False)]
+    out, exp = st.step(e2, tables, 2)
+    close(out[0, :3], exp[0, :3], f"packed step decode rows fp8={fp8}")
+    close(out, exp, f"packed step mixed fp8={fp8}")
+    # step 3: all six decode, one more chunk for the last prompt first
+    e3 = [(41, 1, True), (301, 1, True), (18, 1, True), (150, 1, True), (90, 1, True),
+          (160, 100, False)]
+    out, exp = st.step(e3, tables, 3)
+    close(out, exp, f"packed step 3 fp8={fp8}")
+
+
+def _vl_mrope_prompt(text_before, grid_h, grid_w, text_after):
+    """Explicit (3, n) mRoPE positions of a text + one image + text prompt: text runs
+    t = h = w; the image's patches share t and walk the (h, w) grid; text after the image
+    continues from the largest position + 1 (the Qwen2.5-VL layout)."""
+    cols = []
+    for i in range(text_before):
+        cols.append((i, i, i))
+    s = text_before
+    for r in range(grid_h):
+        for c in range(grid_w):
+            cols.append((s, s + r, s + c))
+    nxt = s + max(grid_h, grid_w)
+    for i in range(text_after):
+        cols.append((nxt + i,) * 3)
+    return torch.tensor(cols, dtype=torch.int64).T.contiguous()
+
+
+def test_qwen25vl_decoder_attention_mrope_prefill_then_decode():
+    torch.manual_seed(12)
+    hidden = 3584
+    m = Qwen25VLDecoderAttention(hidden, 28, num_kv_heads=4, head_dim=128, qkv_bias=True,
+                                 rope_base=1e6, mrope_section=(16, 24, 24))
+    m = m.to("cuda", torch.bfloat16).eval()
+    with torch.no_grad():
+        for lin in (m.q_proj, m.k_proj, m.v_proj):
+            lin.bias.copy_(0.5 * torch.randn_like(lin.bias))
+    m.layer_idx = 0
+    bs, nb = 16, 64
+    kc_g = torch.zeros((1, nb, 4, bs, 128), dtype=torch.bfloat16, device="cuda")
+    vc_g = torch.zeros_like(kc_g)
+    kc_c = torch.zeros((nb, 4, bs, 128), dtype=torch.float64)
+    vc_c = torch.zeros_like(kc_c)
+    mr = [_vl_mrope_prompt(3, 4, 6, 5), _vl_mrope_prompt(0, 8, 8, 2)]
+    plen = [int(x.shape[1]) for x in mr]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(13)).tolist()
+    tables, off = [], 0
+    for L in plen:
+        n = -(-(L + 6) // bs)
+        tables.append(perm[off:off + n])
+        off += n
+    sd = None
+
+    def run(queries, x):
+        nonlocal sd
+        md = meta.build_context(queries)
+        mdg = AttentionMetadata(
+            context_lens=md["context_lens"].cuda(), kv_block_tables=md["kv_block_tables"].cuda(),
+            slot_mapping=md["slot_mapping"].cuda(), k_cache=kc_g, v_cache=vc_g,
+            is_prefill=md["is_prefill"], mrope_position_ids=md["mrope_position_ids"].cuda())
+        with torch.no_grad():
+            out = m(x.cuda(), md["position_ids"].cuda(), md["attention_mask"].cuda(), mdg)
+        torch.cuda.synchronize()
+        q, k, v, sd = cpu_qkv(m, x.double(), md["mrope_position_ids"], mrope=True)
+        a = ref.paged_attention(q, k, v, kc_c, vc_c, md["slot_mapping"], md["kv_block_tables"],
+                                md["context_lens"], md["attention_mask"], md["is_prefill"])
+        exp = a.reshape(x.shape[0], x.shape[1], -1) @ sd["o_proj.weight"].T
+        return out, exp
+
+    toks = [list(range(100, 100 + L)) for L in plen]
+    x = (torch.randn(2, max(plen), hidden) * 0.3).to(torch.bfloat16)
+    qs = [meta.FullQuery(toks[i], [], meta.PREFILL, tables[i], bs, mr[i]) for i in range(2)]
+    out, exp = run(qs, x)
+    for i, L in enumerate(plen):
+        close(out[i, :L], exp[i, :L], f"VL prefill seq {i}")
+    for t in range(1, 4):
+        xd = (torch.randn(2, 1, hidden) * 0.3).to(torch.bfloat16)
+        qd = [meta.FullQuery(toks[i], [7] * t, meta.DECODE, tables[i], bs, mr[i])
+              for i in range(2)]
+        out, exp = run(qd, xd)
+        close(out, exp, f"VL decode step {t}")
+
+
+# ---- teacher forcing against a float64 CPU model --------------------------------------
+
+
+class CpuQwen3:
+    """The Qwen3 decoder (src/nano_inference/models/qwen3.py) in float64 on the CPU, with
+    the GPU model's weights: dense causal attention over whole sequences."""
+
+    def __init__(self, model):
+        self.cfg = model.config
+        self.sd = {k: v.detach().double().cpu() for k, v in model.state_dict().items()}
+        self.inv = model.layers[0].self_attn.rotary.inv_freq.detach().float().cpu()
+
+    @staticmethod
+    def _rms(x, w, eps):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+    def logits(self, ids, rows):
+        cfg, sd = self.cfg, self.sd
+        n = len(ids)
+        x = sd["embed_tokens.weight"][torch.tensor(ids)]
+        pos = torch.arange(n).view(1, n)
+        h, hkv, d = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        for i in range(cfg.num_layers):
+            p = f"layers.{i}."
+            y = self._rms(x, sd[p + "input_norm.weight"], cfg.rms_norm_eps)
+            q = (y @ sd[p + "self_attn.q_proj.weight"].T).view(1, n, h, d)
+            k = (y @ sd[p + "self_attn.k_proj.weight"].T).view(1, n, hkv, d)
+            v = (y @ sd[p + "self_attn.v_proj.weight"].T).view(1, n, hkv, d)
+            q, k = O.qk_norm_rope(q, k, sd[p + "self_attn.q_norm.weight"],
+                                  sd[p + "self_attn.k_norm.weight"], cfg.rms_norm_eps, pos,
+                                  self.inv)
+            a = np.zeros((n, h, d))
+            bnd = tb.causal_bounds(n, n, "top_left")
+            for hh in range(h):
+                a[:, hh] = tb.attend(q[0, :, hh].numpy(), k[0, :, hh // (h // hkv)].numpy(),
+                                     v[0, :, hh // (h // hkv)].numpy(), 1 / math.sqrt(d), bnd)
+            x = x + torch.from_numpy(a).reshape(n, h * d) @ sd[p + "self_attn.o_proj.weight"].T
+            y = self._rms(x, sd[p + "post_attention_norm.weight"], cfg.rms_norm_eps)
+            mlp = Fn.silu(y @ sd[p + "mlp.gate_proj.weight"].T) * (y @ sd[p + "mlp.up_proj.weight"].T)
+            x = x + mlp @ sd[p + "mlp.down_proj.weight"].T
+        y = self._rms(x[rows], sd["norm.weight"], cfg.rms_norm_eps)
+        return y @ sd["lm_head.weight"].T
+
+
+def _teacher_forcing(gen, prompts, new):
+    cpu = CpuQwen3(gen.model)
+    worst = 0.0
+    for prompt, out in zip(prompts, gen.outputs):
+        assert len(out) == new
+        seq = list(prompt) + list(out[:-1])
+        rows = list(range(len(prompt) - 1, len(seq)))
+        lg = cpu.logits(seq, rows)
+        scale = lg.abs().max().item()
+        for i, tok in enumerate(out):
+            row = lg[i]
+            gap = (row.max() - row[tok]).item() / scale
+            worst = max(worst, gap)
+            assert gap <= 2e-2, f"position {i}: chose {tok}, float64 argmax {row.argmax().item()}"
+    print(f"TEACHER largest gap to the float64 maximum: {worst:.3g} of the logit scale",
+          flush=True)
+
+
+def _qwen3_0p6b_two_layers():
+    return e2e.Qwen3Config(num_layers=2)
+
+
+@pytest.mark.parametrize("mixed", [False, True])
+def test_generation_qwen3_0p6b_shape_matches_float64_model(mixed):
+    cfg = _qwen3_0p6b_two_layers()
+    prompts = e2e.config4_prompts(5, 20, 90, cfg.vocab_size, seed=31)
+    new = 6
+    gen = e2e.build(cfg, prompts, max_new_tokens=new, max_prefill_batch=3, seed=7, mixed=mixed,
+                    max_step_tokens=96, chunk=32)
+    st = gen.run(prompts)
+    assert st.generated_tokens == len(prompts) * new
+    _teacher_forcing(gen, prompts, new)
