@@ -10,7 +10,8 @@
  *     Status codes are returned for bad arguments before anything is launched,
  *     so a caller can fail one batch without tearing the process down.
  *   - allocates no device memory: outputs and scratch (`workspace`) belong to
- *     the caller.
+ *     the caller (nia_paged_decode_noalloc uses a fixed array of the library's
+ *     own instead, see there).
  *
  * Index dtypes follow the reference engine's metadata:
  *   slot_mapping int64 with -1 padding, block tables int32 zero-padded,
@@ -50,6 +51,7 @@ extern "C" {
 #define NIA_ERR_WORKSPACE 3        /* workspace missing or smaller than required       */
 #define NIA_ERR_LAUNCH 4           /* the HIP runtime refused the kernel launch        */
 #define NIA_ERR_MISALIGNED 5       /* a pointer or stride breaks 16-byte vector access */
+#define NIA_ERR_SCRATCH_LIMIT 6    /* the call needs more than the library's fixed scratch */
 
 /* Library ABI version; bumped whenever a signature below changes. */
 int32_t nia_abi_version(void);
@@ -111,6 +113,29 @@ int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_s
                          int32_t head_dim, int32_t block_size, int64_t num_blocks,
                          float scale, void* workspace, size_t workspace_bytes,
                          int32_t dtype, void* stream);
+
+/*
+ * Paged decode that allocates nothing and takes no workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops and harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results as nia_paged_decode (bf16 or f32 caches), with the workspace
+ * replaced by a fixed array of NIA_DECODE_SCRATCH_BYTES in the library's device
+ * memory (one per GPU, held until the process ends).  A call whose
+ * nia_paged_decode_workspace_size(...) exceeds it returns NIA_ERR_SCRATCH_LIMIT before
+ * anything is launched.  The first call on a device clears the array's work counters on
+ * `stream`; every completed call leaves them at zero.  All calls on one GPU share the
+ * array: calls that overlap in time on one GPU (other streams, other threads) race.
+ */
+#define NIA_DECODE_SCRATCH_BYTES (32u << 20)
+
+int32_t nia_paged_decode_noalloc(void* out, int64_t out_batch_stride, int64_t out_head_stride,
+                                 const void* q, int64_t q_batch_stride, int64_t q_head_stride,
+                                 const void* k_cache, const void* v_cache,
+                                 const int32_t* block_tables, int32_t bt_stride,
+                                 int32_t max_blocks_per_seq, const int64_t* context_lens,
+                                 int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                 float scale, int32_t dtype, void* stream);
 
 /*
  * Varlen prefill attention over contiguous K/V (causal or not).

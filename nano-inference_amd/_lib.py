@@ -26,6 +26,8 @@ ERR_UNSUPPORTED = 2
 ERR_WORKSPACE = 3
 ERR_LAUNCH = 4
 ERR_MISALIGNED = 5
+ERR_SCRATCH_LIMIT = 6
+DECODE_SCRATCH_BYTES = 32 << 20  # NIA_DECODE_SCRATCH_BYTES
 
 _p = C.c_void_p
 _i32 = C.c_int32
@@ -46,6 +48,11 @@ SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p,
          _i32, _i32, _i32, _i32, _i32, _i64, _f32, _p, _sz, _i32, _p],
+    ),
+    "nia_paged_decode_noalloc": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p,
+         _i32, _i32, _i32, _i32, _i32, _i64, _f32, _i32, _p],
     ),
     "nia_paged_decode_fp8": (
         _i32,

@@ -17,6 +17,8 @@ extern "C" const char* nia_error_string(int32_t status) {
       return "HIP kernel launch failed";
     case NIA_ERR_MISALIGNED:
       return "pointer or stride not aligned for 16-byte vector access";
+    case NIA_ERR_SCRATCH_LIMIT:
+      return "the call needs more scratch than the library's fixed decode array holds";
     default:
       return "unknown status";
   }

@@ -45,6 +45,7 @@
 // 4 * ceil(L / BS) table bytes and the 8-byte context length.
 #include <map>
 #include <mutex>
+#include <vector>
 #include <type_traits>
 #include <utility>
 
@@ -1657,3 +1658,70 @@ extern "C" int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride,
                             workspace, workspace_bytes, NIA_DTYPE_BF16, stream);
 }
 
+// ---- decode without caller memory -------------------------------------------------------
+// The same kernels with their workspace (work counters, partition partials) in a fixed
+// device array of this library instead of caller memory, for callers that cannot
+// allocate (code under graph capture, serving loops that forbid allocation).  Every call
+// on a GPU shares that GPU's copy: the counters are cleared once, at the first call on
+// the device, and every completed call leaves them at zero again (as with a caller's
+// workspace); calls that overlap in time on one GPU race for the array.
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)NIA_DECODE_SCRATCH_BYTES;
+
+}  // namespace
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+__global__ void scratch_clear_kernel(uint32_t* p, int words) {
+  for (int i = threadIdx.x; i < words; i += blockDim.x) p[i] = 0u;
+}
+
+std::mutex g_scratch_mutex;
+std::vector<void*> g_scratch_ptr;  // per device: the device address of `scratch`
+
+// The device address of this GPU's `scratch` (looked up, and its counters cleared on
+// `stream`, at the first call on the device), or null when the lookup fails.
+void* device_scratch(int device, hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if ((size_t)device < g_scratch_ptr.size() && g_scratch_ptr[device]) return g_scratch_ptr[device];
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+  hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(64), 0, stream,
+                     reinterpret_cast<uint32_t*>(ptr), (int)(kCounterBytes / 4));
+  if (hipGetLastError() != hipSuccess) return nullptr;
+  if (g_scratch_ptr.size() <= (size_t)device) g_scratch_ptr.resize(device + 1, nullptr);
+  g_scratch_ptr[device] = ptr;
+  return ptr;
+}
+
+}  // namespace
+
+extern "C" int32_t nia_paged_decode_noalloc(void* out, int64_t out_batch_stride,
+                                            int64_t out_head_stride, const void* q,
+                                            int64_t q_batch_stride, int64_t q_head_stride,
+                                            const void* k_cache, const void* v_cache,
+                                            const int32_t* block_tables, int32_t bt_stride,
+                                            int32_t max_blocks_per_seq,
+                                            const int64_t* context_lens, int32_t batch,
+                                            int32_t num_heads, int32_t num_kv_heads,
+                                            int32_t head_dim, int32_t block_size,
+                                            int64_t num_blocks, float scale, int32_t dtype,
+                                            void* stream) {
+  if (batch < 0 || num_heads <= 0 || max_blocks_per_seq < 0) return NIA_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return NIA_OK;
+  const size_t need = nia_paged_decode_workspace_size(batch, num_heads, max_blocks_per_seq,
+                                                      block_size, head_dim);
+  if (need > kScratchBytes) return NIA_ERR_SCRATCH_LIMIT;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0) return NIA_ERR_LAUNCH;
+  void* ws = device_scratch(device, (hipStream_t)stream);
+  if (!ws) return NIA_ERR_LAUNCH;
+  return paged_decode_entry(out, out_batch_stride, out_head_stride, q, q_batch_stride,
+                            q_head_stride, k_cache, v_cache, nullptr, nullptr, false,
+                            block_tables, bt_stride, max_blocks_per_seq, context_lens, batch,
+                            num_heads, num_kv_heads, head_dim, block_size, num_blocks, scale,
+                            ws, kScratchBytes, dtype, stream);
+}

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 def test_version_and_error_strings():
     lib = _lib.load()
     assert lib.nia_abi_version() == _lib.ABI_VERSION
-    for code in range(6):
+    for code in range(7):
         assert lib.nia_error_string(code)
     assert lib.nia_error_string(0) == b"ok"
     assert lib.nia_error_string(99) == b"unknown status"
@@ -69,6 +69,20 @@ def test_validation_returns_codes_without_launching():
     # paged prefill: block size not a power of two
     assert lib.nia_prefill_paged(p, 8, 8, p, 8, 8, p, p, p, 4, 4, p, p, p, 1, 4, 2, 2, 128, 12,
                                  10, 0.1, 2, 0, None) == _lib.ERR_UNSUPPORTED
+
+
+def test_noalloc_decode_refuses_sizes_beyond_its_scratch_without_launching():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
+    # 4096 sequences x 64 heads x 256 partitions of partials: far beyond the fixed array
+    need = lib.nia_paged_decode_workspace_size(4096, 64, 8192, 16, 128)
+    assert need > _lib.DECODE_SCRATCH_BYTES
+    assert lib.nia_paged_decode_noalloc(p, 0, 0, p, 0, 0, p, p, p, 8192, 8192, p, 4096, 64, 8,
+                                        128, 16, 10, 0.1, 0, None) == _lib.ERR_SCRATCH_LIMIT
+    assert lib.nia_paged_decode_noalloc(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 0, 8, 4, 128, 16,
+                                        10, 0.1, 0, None) == _lib.OK  # empty batch
+    assert lib.nia_paged_decode_noalloc(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, -1, 8, 4, 128, 16,
+                                        10, 0.1, 0, None) == _lib.ERR_INVALID_ARGUMENT
 
 
 def test_workspace_size():
