@@ -150,7 +150,9 @@ int32_t nia_paged_decode_noalloc(void* out, int64_t out_batch_stride, int64_t ou
  * [tokens, heads, head_dim] with element strides (tok, head).
  * Query rows that see no key produce zeros.
  *   max_q_len  upper bound of q_len[s] (sizes the grid; larger is allowed).
- * Supported: dtype bf16; head_dim 64, 80, 96 or 128; num_heads % num_kv_heads == 0.
+ * Supported: dtype bf16 (fp32 softmax and accumulation) or f32 (scores summed in fp64,
+ * softmax and P V in fp32; rows and strides 16-byte aligned); head_dim 64, 80, 96 or
+ * 128; num_heads % num_kv_heads == 0.
  */
 int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
                     const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -171,8 +173,9 @@ int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
  * by nia_kv_write) and reads its keys [0, context_lens[s]) through
  * block_tables exactly as nia_paged_decode does.  `causal` is normally
  * NIA_CAUSAL_BOTTOM_RIGHT; NIA_CAUSAL_NONE lets every row see the whole context.
- * Supported: dtype bf16; head_dim 64, 80, 96 or 128; block_size a power of two
- * in 1..64.
+ * Supported: head_dim 64, 80, 96 or 128; dtype bf16 with block_size a power of two in
+ * 1..64, or f32 with any block_size >= 1 (keys in blocks outside [0, num_blocks) are
+ * skipped).
  */
 int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,
                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,

@@ -40,6 +40,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "prefill_f32.h"
 
 namespace {
 
@@ -845,6 +846,11 @@ bool vec_ok(const void* ptr, int64_t a, int64_t b) {
   return (uintptr_t)ptr % 16 == 0 && a % 8 == 0 && b % 8 == 0;
 }
 
+// fp32 rows are read four elements (16 bytes) at a time.
+bool vec_ok_f32(const void* ptr, int64_t a, int64_t b) {
+  return (uintptr_t)ptr % 16 == 0 && a % 4 == 0 && b % 4 == 0;
+}
+
 }  // namespace
 
 extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
@@ -865,7 +871,37 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
   if (num_seqs == 0 || max_q_len == 0) return NIA_OK;
   if (!out || !q || !k || !v || !q_start || !q_len || !k_start || !k_len)
     return NIA_ERR_INVALID_ARGUMENT;
-  if (dtype != NIA_DTYPE_BF16 || !supported_head_dim(head_dim)) return NIA_ERR_UNSUPPORTED;
+  if (!supported_head_dim(head_dim)) return NIA_ERR_UNSUPPORTED;
+  if (dtype == NIA_DTYPE_F32) {
+    if (!vec_ok_f32(q, q_tok_stride, q_head_stride) || !vec_ok_f32(k, k_tok_stride, k_head_stride) ||
+        !vec_ok_f32(v, v_tok_stride, v_head_stride) ||
+        !vec_ok_f32(out, out_tok_stride, out_head_stride))
+      return NIA_ERR_MISALIGNED;
+    PrefillF32Params f{};
+    f.o = (float*)out;
+    f.o_tok = out_tok_stride;
+    f.o_head = out_head_stride;
+    f.q = (const float*)q;
+    f.q_tok = q_tok_stride;
+    f.q_head = q_head_stride;
+    f.k = (const float*)k;
+    f.k_tok = k_tok_stride;
+    f.k_head = k_head_stride;
+    f.v = (const float*)v;
+    f.v_tok = v_tok_stride;
+    f.v_head = v_head_stride;
+    f.q_start = q_start;
+    f.q_len = q_len;
+    f.k_start = k_start;
+    f.k_len = k_len;
+    f.num_heads = num_heads;
+    f.num_kv_heads = num_kv_heads;
+    f.group = num_heads / num_kv_heads;
+    f.causal = causal;
+    f.scale_log2 = (double)scale * 1.4426950408889634;
+    return launch_prefill_f32(f, false, head_dim, num_seqs, max_q_len, (hipStream_t)stream);
+  }
+  if (dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
   if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(k, k_tok_stride, k_head_stride) ||
       !vec_ok(v, v_tok_stride, v_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride))
     return NIA_ERR_MISALIGNED;
@@ -948,9 +984,39 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
   if (!out || !q || !q_start || !q_len || !context_lens) return NIA_ERR_INVALID_ARGUMENT;
   if (max_blocks_per_seq > 0 && (!k_cache || !v_cache || !block_tables))
     return NIA_ERR_INVALID_ARGUMENT;
-  if (dtype != NIA_DTYPE_BF16 || !supported_head_dim(head_dim)) return NIA_ERR_UNSUPPORTED;
-  if (block_size <= 0 || block_size > 64 || (block_size & (block_size - 1)))
-    return NIA_ERR_UNSUPPORTED;
+  if (!supported_head_dim(head_dim) || block_size <= 0) return NIA_ERR_UNSUPPORTED;
+  if (dtype == NIA_DTYPE_F32) {
+    // any block size: the fp32 kernel maps every key through the table on its own
+    if (!vec_ok_f32(q, q_tok_stride, q_head_stride) ||
+        !vec_ok_f32(out, out_tok_stride, out_head_stride) || (uintptr_t)k_cache % 16 ||
+        (uintptr_t)v_cache % 16)
+      return NIA_ERR_MISALIGNED;
+    PrefillF32Params f{};
+    f.o = (float*)out;
+    f.o_tok = out_tok_stride;
+    f.o_head = out_head_stride;
+    f.q = (const float*)q;
+    f.q_tok = q_tok_stride;
+    f.q_head = q_head_stride;
+    f.k = (const float*)k_cache;
+    f.v = (const float*)v_cache;
+    f.q_start = q_start;
+    f.q_len = q_len;
+    f.ctx_len = context_lens;
+    f.block_tables = block_tables;
+    f.bt_stride = bt_stride;
+    f.max_blocks = max_blocks_per_seq;
+    f.num_blocks = num_blocks;
+    f.block_size = block_size;
+    f.num_heads = num_heads;
+    f.num_kv_heads = num_kv_heads;
+    f.group = num_heads / num_kv_heads;
+    f.causal = causal;
+    f.scale_log2 = (double)scale * 1.4426950408889634;
+    return launch_prefill_f32(f, true, head_dim, num_seqs, max_q_len, (hipStream_t)stream);
+  }
+  if (dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
+  if (block_size > 64 || (block_size & (block_size - 1))) return NIA_ERR_UNSUPPORTED;
   if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride) ||
       (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
     return NIA_ERR_MISALIGNED;

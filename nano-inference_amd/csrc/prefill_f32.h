@@ -1,0 +1,36 @@
+// fp32 prefill kernels (prefill_f32.hip), launched by the nia_prefill / nia_prefill_paged
+// entry points of prefill.hip for NIA_DTYPE_F32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct PrefillF32Params {
+  float* o;
+  int64_t o_tok, o_head;
+  const float* q;
+  int64_t q_tok, q_head;
+  const float* k;  // contiguous K/V rows, or the paged cache slice [NB, H_kv, BS, D]
+  int64_t k_tok, k_head;
+  const float* v;
+  int64_t v_tok, v_head;
+  const int32_t* q_start;
+  const int32_t* q_len;
+  const int32_t* k_start;  // contiguous mode
+  const int32_t* k_len;    // contiguous mode
+  const int64_t* ctx_len;  // paged mode
+  const int32_t* block_tables;
+  int32_t bt_stride;
+  int32_t max_blocks;
+  int64_t num_blocks;
+  int32_t block_size;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t group;
+  int32_t causal;
+  double scale_log2;
+};
+
+// Grid (m-blocks of 64 rows, heads, sequences); returns an NIA_* status.
+int32_t launch_prefill_f32(const PrefillF32Params& p, bool paged, int head_dim, int num_seqs,
+                           int max_q_len, hipStream_t stream);

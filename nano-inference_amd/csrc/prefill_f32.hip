@@ -1,0 +1,231 @@
+// fp32 varlen prefill attention (causal / non-causal, contiguous or paged K/V) for gfx950.
+//
+// The fp32 mode of the reference's attention (its shipped configs run float32,
+// configs/default.yaml:4): the prefill branch of src/nano_inference/layers/attention.py:
+// 281-284 with scaled_dot_product_attention (:12-50), the vision tower's per-chunk loop
+// (src/nano_inference/layers/vision.py:190-208), and chunked prefill over the paged cache.
+// Same varlen description and causal modes as the bf16 kernels (include/nia_attn.h).
+//
+// Precision: every score q . k is summed on the fp64 matrix cores
+// (v_mfma_f64_16x16x4_f64, fp32 inputs widened exactly), so it carries no accumulated
+// rounding even at logits of ~100 nats, where an fp32 sum of 128 products is already
+// ~1e-5 off; the softmax keeps its running max in fp64 and its weights, sums and the
+// output in fp32 (P V on v_mfma_f32_16x16x4_f32).
+//
+// Tiling: a workgroup of 4 waves owns 64 query rows of one head (16 per wave); key
+// tiles of 32 rows are staged through LDS (fp32, rows padded by 4 floats).  Both 16x16x4
+// MFMAs take A[l % 16][l / 16] and B[l / 16][l % 16] from lane l and give it column
+// l % 16 of the 16x16 result; register i holds row 4 (l / 16) + i for fp32 and row
+// 4 i + l / 16 for fp64 (pinned on the device by an in-bounds probe):
+//   S^T = K Q^T (fp64): rows are keys, columns the wave's 16 queries; k step (c, i) of
+//     the contraction pairs lane slot l / 16 with dim 16 c + 4 (l / 16) + i on both
+//     sides (the pairing only has to agree between A and B); register i of a lane is key
+//     4 i + l / 16 of the 16-key tile;
+//   O^T = V^T P^T (fp32): rows are dims, columns queries; k step j pairs slot l / 16
+//     with key 4 j + l / 16, which is exactly the S^T register j a lane already holds, so
+//     P needs no exchange between lanes.
+// A query's 16 scores of a key tile sit in lanes l, l ^ 16, l ^ 32, l ^ 48.
+#include "common.h"
+#include "prefill_f32.h"
+
+namespace {
+
+constexpr int kF32Waves = 4;
+constexpr int kF32Threads = kF32Waves * kWave;
+constexpr int kF32BlockM = 16 * kF32Waves;  // query rows per workgroup
+constexpr int kF32BlockN = 32;              // keys per LDS tile
+
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+
+template <int D, bool PAGED>
+__global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Params p) {
+  static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
+  constexpr int kRow = D + 4;  // LDS row stride in floats
+  constexpr int kC4 = D / 4;   // float4 per row
+  __shared__ __attribute__((aligned(16))) float sk[kF32BlockN * kRow];
+  __shared__ __attribute__((aligned(16))) float sv[kF32BlockN * kRow];
+  __shared__ int sok[kF32BlockN];  // key of the tile lies in a valid block
+
+  const int mb = blockIdx.x;
+  const int h = blockIdx.y;
+  const int seq = blockIdx.z;
+  const int qlen = p.q_len[seq];
+  const int m0 = mb * kF32BlockM;
+  if (qlen <= 0 || m0 >= qlen) return;  // uniform over the workgroup
+  int klen;
+  int64_t kstart = 0;
+  if constexpr (PAGED) {
+    int64_t c = p.ctx_len[seq];
+    const int64_t cap = (int64_t)p.max_blocks * p.block_size;
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    klen = (int)c;
+  } else {
+    klen = p.k_len[seq] > 0 ? p.k_len[seq] : 0;
+    kstart = p.k_start[seq];
+  }
+  const int hk = h / p.group;
+  const bool causal = p.causal != NIA_CAUSAL_NONE;
+  const int q_pos0 = p.causal == NIA_CAUSAL_BOTTOM_RIGHT ? klen - qlen : 0;
+  int n_end = klen;
+  if (causal) n_end = min(klen, max(0, q_pos0 + min(m0 + kF32BlockM, qlen)));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int col = lane & 15;   // the lane's query within the wave's 16
+  const int slot = lane >> 4;  // k slot of the MFMA operands
+  const int r = m0 + 16 * wave + col;
+  const bool row_ok = r < qlen;
+  // keys [0, kb) are visible to this lane's query
+  const int kb = row_ok ? (causal ? min(klen, max(0, q_pos0 + r + 1)) : klen) : 0;
+
+  // B operand of S^T: q[r][16 c + 4 slot + i] widened to fp64
+  double qd[D / 4];
+  {
+    const float* qp = p.q + (p.q_start[seq] + (int64_t)(row_ok ? r : 0)) * p.q_tok +
+                      (int64_t)h * p.q_head;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      const float4 u = row_ok ? *reinterpret_cast<const float4*>(qp + 16 * c + 4 * slot)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      qd[4 * c + 0] = u.x;
+      qd[4 * c + 1] = u.y;
+      qd[4 * c + 2] = u.z;
+      qd[4 * c + 3] = u.w;
+    }
+  }
+
+  f32x4_t oacc[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  double m_run = -INFINITY;  // the query's running max, log2 units
+  float l_run = 0.f;         // this lane's share of the query's sum
+
+  const int32_t* bt = PAGED ? p.block_tables + (int64_t)seq * p.bt_stride : nullptr;
+  for (int n0 = 0; n0 < n_end; n0 += kF32BlockN) {
+    __syncthreads();  // the previous tile is consumed
+    // ---- stage keys n0 .. n0 + 31 (zeros past the context and in invalid blocks) ----------
+    for (int idx = tid; idx < kF32BlockN * kC4; idx += kF32Threads) {
+      const int key = idx / kC4;
+      const int c4 = idx - key * kC4;
+      const int t = n0 + key;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      bool ok = t < klen;
+      if (ok) {
+        const float *kr, *vr;
+        if constexpr (PAGED) {
+          const int blk = bt[t / p.block_size];
+          ok = blk >= 0 && (int64_t)blk < p.num_blocks;
+          const int64_t row =
+              (((int64_t)(ok ? blk : 0) * p.num_kv_heads + hk) * p.block_size + t % p.block_size) * D;
+          kr = p.k + row;
+          vr = p.v + row;
+        } else {
+          kr = p.k + (kstart + t) * p.k_tok + (int64_t)hk * p.k_head;
+          vr = p.v + (kstart + t) * p.v_tok + (int64_t)hk * p.v_head;
+        }
+        if (ok) {
+          kv = *reinterpret_cast<const float4*>(kr + 4 * c4);
+          vv = *reinterpret_cast<const float4*>(vr + 4 * c4);
+        }
+      }
+      *reinterpret_cast<float4*>(sk + key * kRow + 4 * c4) = kv;
+      *reinterpret_cast<float4*>(sv + key * kRow + 4 * c4) = vv;
+      if (c4 == 0) sok[key] = ok;
+    }
+    __syncthreads();
+    if (!wave_any(n0 < kb)) continue;  // no query of this wave sees the tile
+
+    // ---- S^T = K Q^T in fp64, two 16-key tiles ----------------------------------------------
+    f64x4_t s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      s[kt] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+      const float* kr = sk + (16 * kt + col) * kRow + 4 * slot;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        const float4 a = *reinterpret_cast<const float4*>(kr + 16 * c);
+        s[kt] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.x, qd[4 * c + 0], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.y, qd[4 * c + 1], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.z, qd[4 * c + 2], s[kt], 0, 0, 0);
+        s[kt] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.w, qd[4 * c + 3], s[kt], 0, 0, 0);
+      }
+    }
+    // ---- online softmax: lane register i of tile kt is key n0 + 16 kt + 4 i + slot ----------
+    double x[2][4];
+    double mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = 16 * kt + 4 * i + slot;
+        const bool vis = n0 + key < kb && sok[key];
+        x[kt][i] = vis ? s[kt][i] * p.scale_log2 : -INFINITY;
+        mx = fmax(mx, x[kt][i]);
+      }
+    mx = fmax(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmax(mx, __shfl_xor(mx, 32, kWave));
+    const double mn = fmax(m_run, mx);
+    if (mn > m_run) {  // lane-uniform within the query's four lanes
+      const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2((float)(m_run - mn));
+      m_run = mn;
+      l_run *= corr;
+#pragma unroll
+      for (int t = 0; t < D / 16; ++t) oacc[t] *= corr;
+    }
+    float pr[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[kt][i] = x[kt][i] == -INFINITY ? 0.f : fast_exp2((float)(x[kt][i] - m_run));
+        l_run += pr[kt][i];
+      }
+    // ---- O^T += V^T P^T ----------------------------------------------------------------------
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float* vr = sv + (16 * kt + 4 * j + slot) * kRow + col;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t)
+          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * t], pr[kt][j], oacc[t], 0, 0, 0);
+      }
+  }
+
+  // ---- normalise and store: lane l holds dims 16 t + 4 slot .. + 3 of query col ------------
+  l_run += __shfl_xor(l_run, 16, kWave);
+  l_run += __shfl_xor(l_run, 32, kWave);
+  if (!row_ok) return;
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  float* op = p.o + (p.q_start[seq] + (int64_t)r) * p.o_tok + (int64_t)h * p.o_head;
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t)
+    *reinterpret_cast<float4*>(op + 16 * t + 4 * slot) =
+        make_float4(oacc[t][0] * inv, oacc[t][1] * inv, oacc[t][2] * inv, oacc[t][3] * inv);
+}
+
+}  // namespace
+
+int32_t launch_prefill_f32(const PrefillF32Params& p, bool paged, int head_dim, int num_seqs,
+                           int max_q_len, hipStream_t stream) {
+  if (num_seqs > 65535 || p.num_heads > 65535) return NIA_ERR_UNSUPPORTED;
+  const dim3 grid((max_q_len + kF32BlockM - 1) / kF32BlockM, p.num_heads, num_seqs);
+  switch (head_dim) {
+#define NIA_F32_CASE(DD)                                                                      \
+  case DD:                                                                                    \
+    if (paged)                                                                                \
+      hipLaunchKernelGGL((prefill_f32_kernel<DD, true>), grid, dim3(kF32Threads), 0, stream, p); \
+    else                                                                                      \
+      hipLaunchKernelGGL((prefill_f32_kernel<DD, false>), grid, dim3(kF32Threads), 0, stream, p); \
+    break;
+    NIA_F32_CASE(64)
+    NIA_F32_CASE(80)
+    NIA_F32_CASE(96)
+    NIA_F32_CASE(128)
+#undef NIA_F32_CASE
+    default:
+      return NIA_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+}

@@ -296,7 +296,7 @@ def prefill(
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Varlen attention over contiguous K/V rows (nia_prefill).
+    """Varlen attention over contiguous K/V rows (nia_prefill), bf16 or fp32.
 
     q/out: (Tq, H, D); k/v: (Tk, H_kv, D), each with a contiguous last dim.
     Sequence s owns query rows q_start[s] .. + q_len[s] and key rows
@@ -314,7 +314,7 @@ def prefill(
         raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k and v must share one dtype")
-    dt = _dtype_code(q, (torch.bfloat16,))
+    dt = _dtype_code(q)
     for name, t in (("q", q), ("k", k), ("v", v)):
         _last_contig(name, t)
     n = q_start.shape[0]
@@ -388,7 +388,7 @@ def prefill_paged(
     k_scale: Optional[torch.Tensor] = None,
     v_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Query chunks against their paged keys (nia_prefill_paged).
+    """Query chunks against their paged keys (nia_prefill_paged), bf16 or fp32.
 
     q/out: (Tq, H, D).  Sequence s has q_len[s] query rows starting at token
     q_start[s], sitting at absolute positions context_lens[s] - q_len[s] + j,
@@ -414,7 +414,7 @@ def prefill_paged(
         raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
     if not (q.dtype == k_cache.dtype == v_cache.dtype):
         raise ValueError("q and the caches must share one dtype")
-    dt = _dtype_code(q, (torch.bfloat16,))
+    dt = _dtype_code(q)
     _last_contig("q", q)
     n = q_start.shape[0]
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != n:

@@ -58,9 +58,11 @@ def test_validation_returns_codes_without_launching():
     # decode: workspace too small for 2 partitions
     assert lib.nia_paged_decode(p, 128, 128, p, 1024, 128, p, p, p, 64, 64, p, 2, 8, 4, 128, 16,
                                 100, 0.1, None, 0, 0, None) == _lib.ERR_WORKSPACE
-    # prefill: fp32 has no MFMA kernel
+    # prefill: unknown dtype; fp32 rows whose strides break 16-byte loads
     assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.1,
-                           1, 1, None) == _lib.ERR_UNSUPPORTED
+                           1, 7, None) == _lib.ERR_UNSUPPORTED
+    assert lib.nia_prefill(p, 8, 8, p, 6, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.1,
+                           1, 1, None) == _lib.ERR_MISALIGNED
     # prefill: bad causal mode, non-positive scale
     assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.1,
                            5, 0, None) == _lib.ERR_INVALID_ARGUMENT
