@@ -128,8 +128,8 @@ def bench_decode(torch, ops, workloads, steps: int, warmup: int):
     c = workloads.decode_qwen3_8b("cuda", layers=DECODE_LAYERS)
     b, h, d = c.q.shape
     out = torch.empty_like(c.q)
-    ws = torch.zeros(ops.decode_workspace_bytes(b, h, c.block_tables.shape[1], 16, d),
-                     dtype=torch.uint8, device="cuda")
+    ws = torch.empty(ops.decode_workspace_bytes(b, h, c.num_kv_heads, c.block_tables.shape[1],
+                                                16, d), dtype=torch.uint8, device="cuda")
 
     def write(i):
         L = i % DECODE_LAYERS

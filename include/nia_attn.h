@@ -88,21 +88,22 @@ int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
  * block_tables[b, t / block_size], offset t % block_size.
  * Keys at t >= L_b are never read, so padded table entries (the reference reads
  * block 0 there and masks it) cannot affect the output.  Sequences with L_b <= 0
- * produce zeros.  Block ids outside [0, num_blocks) are skipped.
+ * produce zeros.  Keys in blocks with ids outside [0, num_blocks) are skipped.
  *   q, out       [batch, num_heads, head_dim] with element strides (batch, head).
  *   block_tables [batch, bt_stride] int32, the first max_blocks_per_seq columns used.
  *   workspace    >= nia_paged_decode_workspace_size(...) bytes of device memory,
- *                256-byte aligned.  Its leading bytes hold work counters: the
- *                whole workspace must be zero before its first use; every call
- *                that completes leaves the counters at zero again, so one
- *                workspace serves any number of calls issued one after another
- *                (calls that overlap in time need workspaces of their own).
- * Supported: head_dim 128; block_size 16; num_heads / num_kv_heads in 1..8;
- * dtype bf16 (fp32 softmax and accumulation) or f32.
+ *                256-byte aligned (partial results; nothing in it needs to be
+ *                initialised).  Calls that overlap in time need workspaces of their
+ *                own; calls issued one after another may share one.
+ * Supported:
+ *   dtype bf16 (fp32 softmax and accumulation): block_size a power of two >= 4,
+ *     head_dim 64, 80, 96 or 128, num_heads / num_kv_heads in 1..16;
+ *   dtype f32 (q . k summed in fp64): any block_size, head_dim 64, 80, 96 or 128, any
+ *     num_heads / num_kv_heads.
  */
-size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_heads,
+size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t num_kv_heads,
                                        int32_t max_blocks_per_seq, int32_t block_size,
-                                       int32_t head_dim);
+                                       int32_t head_dim, int32_t dtype);
 
 int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_stride,
                          const void* q, int64_t q_batch_stride, int64_t q_head_stride,
@@ -122,9 +123,9 @@ int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_s
  * replaced by a fixed array of NIA_DECODE_SCRATCH_BYTES in the library's device
  * memory (one per GPU, held until the process ends).  A call whose
  * nia_paged_decode_workspace_size(...) exceeds it returns NIA_ERR_SCRATCH_LIMIT before
- * anything is launched.  The first call on a device clears the array's work counters on
- * `stream`; every completed call leaves them at zero.  All calls on one GPU share the
- * array: calls that overlap in time on one GPU (other streams, other threads) race.
+ * anything is launched.  The first call on a device clears the array's header on
+ * `stream`.  All calls on one GPU share the array: calls that overlap in time on one
+ * GPU (other streams, other threads) race.
  */
 #define NIA_DECODE_SCRATCH_BYTES (32u << 20)
 
@@ -273,11 +274,12 @@ int32_t nia_qk_norm_rope_kv_write_fp8(void* q, int64_t q_tok_stride, int64_t q_h
 /*
  * Paged decode over fp8 caches: nia_paged_decode with k_cache / v_cache in the fp8
  * format above (uint8 codes, k_scale / v_scale fp32 [num_blocks, num_kv_heads,
- * block_size], 16-byte aligned, else NIA_ERR_MISALIGNED).  q and out are bf16; keys are dequantised exactly as
- * code * row scale (the code is widened to bf16 without rounding, the scale
- * multiplies the q . k score, and each softmax weight carries its row's v scale).
- * Same workspace contract and shapes as nia_paged_decode (head_dim 128, block
- * size 16, num_heads / num_kv_heads <= 8).
+ * block_size], 16-byte aligned, else NIA_ERR_MISALIGNED).  q and out are bf16; keys
+ * are dequantised exactly as code * row scale (the code is widened to bf16 without
+ * rounding, the scale multiplies the q . k score, and each softmax weight carries its
+ * row's v scale).  Same workspace contract as nia_paged_decode (its size with dtype
+ * NIA_DTYPE_BF16); head_dim 128, block_size a power of two >= 16, num_heads /
+ * num_kv_heads <= 16.
  */
 int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride, int64_t out_head_stride,
                              const void* q, int64_t q_batch_stride, int64_t q_head_stride,

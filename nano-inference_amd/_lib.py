@@ -43,7 +43,7 @@ SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i32, _p],
     ),
-    "nia_paged_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "nia_paged_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "nia_paged_decode": (
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p,
@@ -100,7 +100,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: C.CDLL | None = None

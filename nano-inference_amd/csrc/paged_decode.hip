@@ -1,5 +1,5 @@
-// Split-K paged decode attention for gfx950 (HBM-bound; the matrix cores only take the
-// dot products off the vector unit).
+// Paged decode attention for gfx950 (HBM-bound; the matrix cores only take the dot
+// products off the vector unit).
 //
 // Replaces the decode branch of the reference, src/nano_inference/layers/
 // attention.py:285-332: a padded gather of every sequence's K/V through the
@@ -8,48 +8,42 @@
 // Here each KV byte is read from HBM exactly once and shared by the G query
 // heads of its group.
 //
-// Two kernels compute partial attention over partitions of a sequence's blocks;
-// paged_decode_combine_kernel merges the partials (one wave per (sequence, head)).
-//
-// Shapes: D = 128, BS = 16, G = H / H_kv <= 8 (others return NIA_ERR_UNSUPPORTED).
-// bf16 (the serving path)
-//   Work items are (sequence, partition of <= 32 blocks, or <= 48 when the batch holds
-//   at least 6 items per persistent workgroup, KV head), numbered on the
-//   device from context_lens; persistent workgroups (2 per CU) take them from an
-//   atomic ticket (paged_decode_bf16_persistent_kernel), or the grid enumerates
-//   them for batches above 4096 (paged_decode_bf16_kernel).  An item's 4 waves take
-//   the partition's block pairs round-robin.
-//   Batches of at most 1024 (bf16 and fp8 caches): decode_item_mfma.  A wave's block
-//   pair streams into its 16 KB LDS slot by DMA while the previous pair is computed;
-//   scores S^T = K Q^T and O^T += V^T P^T run on 16x16 MFMAs with the group's heads as
-//   columns.
-//   Larger batches: decode_item on the vector unit.  Per pair a wave
-//   issues 16 wave-wide 16-byte loads (K and V of two 4 KB block-heads), and for
-//   G <= 4 the next pair's K goes out right after this pair's scores, its V right after
-//   this pair's P V.  K layout: 8 lanes per token, two tokens per lane, so q . k is 8
-//   v_dot2_f32_bf16 plus a 3-step DPP sum.  V layout: 16 lanes per token (8 dims each),
-//   so P V is v_dot2_f32_bf16 over the pair's two blocks with the weights packed as a
-//   bf16 pair and moved from the K lanes to the V lanes with ds_bpermute.
-// fp32 (same shapes)
-//   paged_decode_partial_kernel: grid (partition, KV head, sequence); wave w takes
-//   blocks w, w + 4, ... of the partition; 32 lanes per token in one layout for
-//   both K and V; q . k is summed in fp64.
-// Softmax (both)
-//   Scores are kept in log2 units (scale * log2 e folded in).  Each lane row keeps
-//   its own running (l, o[8 dims]) against a running max (per lane row in fp32, one
-//   per wave and head in bf16) that is only raised when a block's max exceeds it
-//   by more than kLazyRescale (2^8),
-//   which keeps the O rescale off the common path and bounds p by 2^8.  At the end
-//   rows merge by shuffles, waves through LDS, partitions in the combine kernel.
+// bf16 caches and the fp8 cache format: decode_split_kernel + decode_split_combine_kernel.
+//   The keys of every (sequence, KV head) are cut into units of 32 (a pair of 16-key
+//   tiles).  KV heads are taken hg at a time (hg = 4, 2 or 1, dividing H_kv) and units
+//   are numbered head group major: unit (g, b, j) = g * T + pfx[b] + j, where pfx is the
+//   prefix sum over sequences of their unit counts and T = pfx[batch], built on the
+//   device from context_lens.  A workgroup is 4 waves = hg KV heads x wph = 4 / hg
+//   slices; "virtual wave" vw = w * wph + slice owns one KV head of the group and the
+//   contiguous unit range [total * vw / V, total * (vw + 1) / V), V = grid * wph, of a
+//   grid of resident workgroups.  Every wave streams its range alone (no work queue, no
+//   barrier, no cross-wave merge): pairs of tiles DMA (buffer loads into LDS) into its
+//   16 KB slot one pair ahead, S^T = K Q^T and O^T += V^T P^T run on 16x16 MFMAs with the
+//   group's G <= 16 query heads as columns, and at the end of every sequence of its range
+//   the wave writes the output (it had the whole sequence) or a partial (m, l, o) that
+//   the combine kernel merges.  The ranges are equal, so no workgroup waits on a long
+//   last item, and with hg = 4 the 4 waves of a workgroup read the 4 adjacent KV heads
+//   of the same blocks (16 KB contiguous per block for K and for V).
+//   Shapes: block size a power of two >= 4 (>= 16 for fp8), head_dim 64 / 80 / 96 / 128
+//   (fp8: 128), G <= 16.
+// fp32 caches (the reference's CPU default; tolerance 1e-5):
+//   head_dim 128, block size 16, G <= 8: paged_decode_partial_kernel, grid (partition,
+//   KV head, sequence); wave w takes blocks w, w + 4, ... of the partition; 32 lanes per
+//   token; q . k is summed in fp64; partials merged by paged_decode_combine_kernel.
+//   Other fp32 shapes run the fp32 prefill kernel with one query row per sequence.
+// Softmax (all): scores in log2 units (scale * log2 e applied in fp32 to the raw
+// scores).  A running max is only raised when a block exceeds it by more than
+// kLazyRescale (2^8), which keeps the O rescale off the common path and bounds p by 2^8.
 // Algorithmic HBM bytes per sequence: 2 * L * H_kv * D * s (K and V) plus q, out,
 // 4 * ceil(L / BS) table bytes and the 8-byte context length.
 #include <map>
 #include <mutex>
-#include <vector>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 #include "common.h"
+#include "prefill_f32.h"
 
 namespace {
 
@@ -57,19 +51,6 @@ constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = kDecodeWaves * kWave;
 constexpr int kCombineThreads = 256;  // four (sequence, head) pairs per workgroup
 constexpr float kLazyRescale = 8.0f;
-// Largest query-group size whose block loop keeps the next pair's K in flight
-// during P V (32 more VGPRs than the plain loop).
-constexpr int kRollingMaxG = 4;
-
-// Workgroups per CU of the persistent kernel.  Two (8 waves, a 256-VGPR budget)
-// for bf16 caches and large groups; fp8 caches with G <= 4 run the plain loop at
-// three (12 waves): a pair of fp8 block-heads is half the bytes, so more waves
-// keep enough loads in flight (measured 152 -> 142 us on the Qwen3-8B workload;
-// the rolling loop does not fit three waves' registers).
-constexpr int persistent_waves(int G, bool fp8) { return fp8 && G <= kRollingMaxG ? 3 : 2; }
-constexpr bool rolling_loop(int G, bool fp8) {
-  return G <= kRollingMaxG && persistent_waves(G, fp8) == 2;
-}
 
 struct DecodeParams {
   void* out;
@@ -88,9 +69,20 @@ struct DecodeParams {
   int32_t num_kv_heads;
   int64_t num_blocks;
   float scale_log2;
+  // fp32 partition kernel
   float* ws_ml;  // [batch][num_heads][max_parts][2]  (m, l) in log2 units
   float* ws_o;   // [batch][num_heads][max_parts][D]   un-normalised partial output
   int32_t max_parts;
+  // split kernel
+  int32_t bs_log2;
+  int32_t group;  // G = num_heads / num_kv_heads
+  int32_t hg;     // KV heads per workgroup
+  int32_t wph;    // slices per KV head (4 / hg)
+  int32_t nhg;    // head groups (num_kv_heads / hg)
+  int32_t grid;   // workgroups
+  int32_t* ws_pfx;  // [batch + 1] units before each sequence (one head group)
+  float* sp_ml;     // [grid * wph][2][hg][G] (m, l) of the partial of a range's first / last sequence
+  float* sp_o;      // [grid * wph][2][hg][G][D]
 };
 
 // Element-type specific pieces: how 16 loaded bytes enter a dot product and
@@ -494,763 +486,6 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine_kernel(D
   out[1] = E::from_f32(acc.y * inv);
 }
 
-// Decode with head_dim 128, block size 16 (the serving layout), bf16 queries, and
-// the cache in bf16 or in the fp8 format (e4m3 codes, one fp32 scale per row).
-//
-// Two lane layouts share one wave:
-//   K layout: 8 lanes per token; a lane owns 2 tokens per block (l / 8 and
-//     l / 8 + 8) and 16 dims (16 (l % 8) .. +15), so a q . k dot product is 8 bf16
-//     dot2 per lane and a 3-step DPP sum over 8 lanes.  bf16: 4 wave-wide 16-byte
-//     loads per block-head; fp8: 2 (the 16 codes of a lane, converted to bf16 pairs
-//     with v_cvt_scalef32_pk_bf16_fp8, exact) and the row's k scale multiplies the
-//     score.
-//   V layout: 16 lanes per token, fully coalesced: load i reads token 4i + l/16,
-//     dims 8 (l % 16) .. +7 (16 bytes in bf16, 8 in fp8).
-// Blocks are processed in pairs (A, B).  For each K-layout token the softmax
-// weights of blocks A and B are packed into one bf16 pair and moved to the
-// V-layout lanes with ds_bpermute; there P.V is v_dot2_f32_bf16 over the
-// (A, B) token pair, with V's two tokens interleaved by v_perm (fp8: the codes
-// are interleaved first, then converted, and each weight carries its row's v
-// scale while l sums the unscaled weights).  The running max is uniform over
-// the wave (raised lazily by more than 2^8), so row and lane partials add
-// without rescaling.
-template <int G>
-struct DecodeState {
-  uint32_t qw[G][8];
-  float o[G][8];
-  float l[G];
-  float m[G];
-};
-
-// One block-head in registers: bf16 K (K layout) and V (V layout), fp8 K and V
-// codes plus the row scales of the lane's two K-layout tokens.
-struct KRegs16 { uint4 r[4]; };
-struct VRegs16 { uint4 r[4]; };
-struct KRegs8 { uint4 r[2]; float ks[2]; float vs[2]; };
-struct VRegs8 { uint2 r[4]; };
-
-template <bool FP8> struct KvRegs;
-template <> struct KvRegs<false> { using K = KRegs16; using V = VRegs16; };
-template <> struct KvRegs<true> { using K = KRegs8; using V = VRegs8; };
-
-// Physical block of partition-relative block jx (its table entry sits in lane
-// jx - blk_begin of my_bt), or -1 past the partition or for an invalid id.
-NIA_DEVICE int decode_block_id(const DecodeParams& p, int my_bt, int jx, int blk_begin,
-                               int blk_end) {
-  const int blk = jx < blk_end ? __builtin_amdgcn_readlane(my_bt, jx - blk_begin) : -1;
-  return (blk >= 0 && (int64_t)blk < p.num_blocks) ? blk : -1;
-}
-
-// First element of block-head (blk, hk) of a cache with `row_bytes` per row.
-NIA_DEVICE const uint8_t* block_head(const void* cache, const DecodeParams& p, int blk, int hk,
-                                     int row_bytes) {
-  return reinterpret_cast<const uint8_t*>(cache) +
-         ((int64_t)blk * p.num_kv_heads + hk) * 16 * row_bytes;
-}
-
-// K of one block-head in the K layout; zeros for blk < 0.
-NIA_DEVICE void decode_load_k(const DecodeParams& p, int blk, int hk, int lane, KRegs16& kr) {
-  const int ktok = lane >> 3, kc = lane & 7;
-  if (blk >= 0) {
-    const uint4* kp = reinterpret_cast<const uint4*>(block_head(p.k_cache, p, blk, hk, 256));
-    kr.r[0] = kp[ktok * 16 + 2 * kc];
-    kr.r[1] = kp[ktok * 16 + 2 * kc + 1];
-    kr.r[2] = kp[(ktok + 8) * 16 + 2 * kc];
-    kr.r[3] = kp[(ktok + 8) * 16 + 2 * kc + 1];
-  } else {
-    kr.r[0] = kr.r[1] = kr.r[2] = kr.r[3] = make_uint4(0, 0, 0, 0);
-  }
-}
-
-NIA_DEVICE void decode_load_k(const DecodeParams& p, int blk, int hk, int lane, KRegs8& kr) {
-  const int ktok = lane >> 3, kc = lane & 7;
-  if (blk >= 0) {
-    const uint8_t* kp = block_head(p.k_cache, p, blk, hk, 128);
-    kr.r[0] = *reinterpret_cast<const uint4*>(kp + ktok * 128 + 16 * kc);
-    kr.r[1] = *reinterpret_cast<const uint4*>(kp + (ktok + 8) * 128 + 16 * kc);
-    const int64_t row0 = ((int64_t)blk * p.num_kv_heads + hk) * 16;
-    kr.ks[0] = p.k_scale[row0 + ktok];
-    kr.ks[1] = p.k_scale[row0 + ktok + 8];
-    kr.vs[0] = p.v_scale[row0 + ktok];
-    kr.vs[1] = p.v_scale[row0 + ktok + 8];
-  } else {
-    kr.r[0] = kr.r[1] = make_uint4(0, 0, 0, 0);
-    kr.ks[0] = kr.ks[1] = kr.vs[0] = kr.vs[1] = 0.f;
-  }
-}
-
-// V of one block-head in the V layout; zeros for blk < 0.
-NIA_DEVICE void decode_load_v(const DecodeParams& p, int blk, int hk, int lane, VRegs16& vr) {
-  if (blk >= 0) {
-    const uint4* vp = reinterpret_cast<const uint4*>(block_head(p.v_cache, p, blk, hk, 256));
-    vr.r[0] = vp[lane];
-    vr.r[1] = vp[64 + lane];
-    vr.r[2] = vp[128 + lane];
-    vr.r[3] = vp[192 + lane];
-  } else {
-    vr.r[0] = vr.r[1] = vr.r[2] = vr.r[3] = make_uint4(0, 0, 0, 0);
-  }
-}
-
-NIA_DEVICE void decode_load_v(const DecodeParams& p, int blk, int hk, int lane, VRegs8& vr) {
-  if (blk >= 0) {
-    const uint2* vp = reinterpret_cast<const uint2*>(block_head(p.v_cache, p, blk, hk, 128));
-    vr.r[0] = vp[lane];
-    vr.r[1] = vp[64 + lane];
-    vr.r[2] = vp[128 + lane];
-    vr.r[3] = vp[192 + lane];
-  } else {
-    vr.r[0] = vr.r[1] = vr.r[2] = vr.r[3] = make_uint2(0, 0);
-  }
-}
-
-// Zero the V rows of one 16-token block (V layout) that lie past the context
-// or belong to an invalid block id: stale slots may hold any bits (NaN codes
-// included), and 0 * NaN would poison the sums.
-template <typename VRegs>
-NIA_DEVICE void zero_invalid_v(VRegs& v, bool ok, int tok0, int ctx, int vrow) {
-  if (ok && tok0 + 16 <= ctx) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bool valid = ok && (tok0 + 4 * i + vrow) < ctx;
-    if constexpr (std::is_same<VRegs, VRegs16>::value) {
-      v.r[i].x = valid ? v.r[i].x : 0u;
-      v.r[i].y = valid ? v.r[i].y : 0u;
-      v.r[i].z = valid ? v.r[i].z : 0u;
-      v.r[i].w = valid ? v.r[i].w : 0u;
-    } else {
-      v.r[i].x = valid ? v.r[i].x : 0u;
-      v.r[i].y = valid ? v.r[i].y : 0u;
-    }
-  }
-}
-
-// The 8 bf16 pairs of one K-layout token (16 dims) and its score multiplier.
-NIA_DEVICE void k_token_pairs(const KRegs16& k, int sl, uint32_t (&w)[8]) {
-  const uint4 a = k.r[2 * sl], b = k.r[2 * sl + 1];
-  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-}
-
-NIA_DEVICE void k_token_pairs(const KRegs8& k, int sl, uint32_t (&w)[8]) {
-  const uint4 a = k.r[sl];
-  w[0] = bf16x2_from_fp8x2<false>(a.x);
-  w[1] = bf16x2_from_fp8x2<true>(a.x);
-  w[2] = bf16x2_from_fp8x2<false>(a.y);
-  w[3] = bf16x2_from_fp8x2<true>(a.y);
-  w[4] = bf16x2_from_fp8x2<false>(a.z);
-  w[5] = bf16x2_from_fp8x2<true>(a.z);
-  w[6] = bf16x2_from_fp8x2<false>(a.w);
-  w[7] = bf16x2_from_fp8x2<true>(a.w);
-}
-
-NIA_DEVICE float k_token_scale(const KRegs16&, int) { return 1.f; }
-NIA_DEVICE float k_token_scale(const KRegs8& k, int sl) { return k.ks[sl]; }
-NIA_DEVICE float v_token_scale(const KRegs16&, int) { return 1.f; }
-NIA_DEVICE float v_token_scale(const KRegs8& k, int sl) { return k.vs[sl]; }
-
-// Scores of a block pair (K layout), pre-scaled to log2 units; -inf past the
-// context or in an invalid block.
-template <int G, typename KRegs>
-NIA_DEVICE void decode_qk_pair(const DecodeParams& p, const DecodeState<G>& st, const KRegs& kA,
-                               const KRegs& kB, bool okA, bool okB, int jb, int ctx, int lane,
-                               float (&xs)[2][2][G]) {
-  constexpr int BS = 16;
-  const int ktok = lane >> 3;
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
-      const bool valid = (x ? okB : okA) && ((jb + x) * BS + 8 * sl + ktok) < ctx;
-      uint32_t w[8];
-      k_token_pairs(x ? kB : kA, sl, w);
-      const float mult = k_token_scale(x ? kB : kA, sl) * p.scale_log2;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float s = dot2_bf16(st.qw[g][0], w[0], 0.f);
-#pragma unroll
-        for (int e = 1; e < 8; ++e) s = dot2_bf16(st.qw[g][e], w[e], s);
-        s = group_sum<8>(s);
-        xs[x][sl][g] = valid ? s * mult : -INFINITY;
-      }
-    }
-  }
-}
-
-// O += P V over one V-layout load i (4 tokens of blocks A and B): pv[g] holds the
-// lane's token weights (A, B) as a bf16 pair.
-template <int G>
-NIA_DEVICE void pv_accumulate(DecodeState<G>& st, const uint32_t (&pv)[G], const VRegs16& vA,
-                              const VRegs16& vB, int i) {
-  const uint32_t va[4] = {vA.r[i].x, vA.r[i].y, vA.r[i].z, vA.r[i].w};
-  const uint32_t vb[4] = {vB.r[i].x, vB.r[i].y, vB.r[i].z, vB.r[i].w};
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);
-    const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      st.o[g][2 * w] = dot2_bf16(pv[g], lo, st.o[g][2 * w]);
-      st.o[g][2 * w + 1] = dot2_bf16(pv[g], hi, st.o[g][2 * w + 1]);
-    }
-  }
-}
-
-template <int G>
-NIA_DEVICE void pv_accumulate(DecodeState<G>& st, const uint32_t (&pv)[G], const VRegs8& vA,
-                              const VRegs8& vB, int i) {
-  const uint32_t va[2] = {vA.r[i].x, vA.r[i].y};
-  const uint32_t vb[2] = {vB.r[i].x, vB.r[i].y};
-#pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    // codes (a0 b0 a1 b1) and (a2 b2 a3 b3), then (A, B) bf16 pairs per dim
-    const uint32_t lo = __builtin_amdgcn_perm(vb[w], va[w], 0x05010400u);
-    const uint32_t hi = __builtin_amdgcn_perm(vb[w], va[w], 0x07030602u);
-    const uint32_t d[4] = {bf16x2_from_fp8x2<false>(lo), bf16x2_from_fp8x2<true>(lo),
-                           bf16x2_from_fp8x2<false>(hi), bf16x2_from_fp8x2<true>(hi)};
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < G; ++g) st.o[g][4 * w + j] = dot2_bf16(pv[g], d[j], st.o[g][4 * w + j]);
-  }
-}
-
-// Online-softmax update and O += P V for a block pair (V layout).  kA, kB supply
-// the fp8 rows' v scales (K layout); the weights that multiply V carry them.
-template <int G, typename KRegs, typename VRegs>
-NIA_DEVICE void decode_pv_pair(const DecodeParams& p, DecodeState<G>& st,
-                               const float (&xs)[2][2][G], const KRegs& kA, const KRegs& kB,
-                               VRegs& vA, VRegs& vB, bool okA, bool okB, int jb, int ctx,
-                               int lane) {
-  constexpr int BS = 16;
-  constexpr bool kScaled = std::is_same<KRegs, KRegs8>::value;
-  const int vrow = lane >> 4;
-  const int ktok = lane >> 3;
-  // ---- lazy wave-uniform running max -------------------------------------------------------
-  float bm[G];
-  bool need = false;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    bm[g] = fmaxf(fmaxf(xs[0][0][g], xs[0][1][g]), fmaxf(xs[1][0][g], xs[1][1][g]));
-    need |= bm[g] > st.m[g] + kLazyRescale;
-  }
-  if (wave_any(need)) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mn = fmaxf(st.m[g], wave_max(bm[g]));
-      const float corr = (st.m[g] == -INFINITY) ? 0.f : fast_exp2(st.m[g] - mn);
-      st.m[g] = mn;
-      st.l[g] *= corr;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) st.o[g][e] *= corr;
-    }
-  }
-  // ---- weights, packed (A, B) per token ----------------------------------------------------
-  float vsa[2], vsb[2];
-#pragma unroll
-  for (int sl = 0; sl < 2; ++sl) {
-    if constexpr (kScaled) {
-      // a stale row's scale may be any value: weights past the context are 0 * 0
-      vsa[sl] = okA && (jb * BS + 8 * sl + ktok) < ctx ? v_token_scale(kA, sl) : 0.f;
-      vsb[sl] = okB && ((jb + 1) * BS + 8 * sl + ktok) < ctx ? v_token_scale(kB, sl) : 0.f;
-    } else {
-      vsa[sl] = vsb[sl] = 1.f;
-    }
-  }
-  uint32_t pp[2][G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float msub = (st.m[g] == -INFINITY) ? 0.f : st.m[g];
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
-      const float pa = fast_exp2(xs[0][sl][g] - msub);
-      const float pb2 = fast_exp2(xs[1][sl][g] - msub);
-      st.l[g] += pa + pb2;
-      pp[sl][g] = kScaled ? pack_bf16x2(pa * vsa[sl], pb2 * vsb[sl]) : pack_bf16x2(pa, pb2);
-    }
-  }
-  zero_invalid_v(vA, okA, jb * BS, ctx, vrow);
-  zero_invalid_v(vB, okB, (jb + 1) * BS, ctx, vrow);
-  // ---- O += P V (V layout) -----------------------------------------------------------------
-  // ds_bpermute byte addresses: V-layout load i reads the K-layout lane that
-  // owns its token, 8 * (4 (i % 2) + l / 16), from slot i / 2.
-  const int bp_addr0 = (8 * vrow) * 4;
-  const int bp_addr1 = (8 * (4 + vrow)) * 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t pv[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      pv[g] = (uint32_t)__builtin_amdgcn_ds_bpermute((i & 1) ? bp_addr1 : bp_addr0,
-                                                     (int)pp[i >> 1][g]);
-    pv_accumulate<G>(st, pv, vA, vB, i);
-  }
-}
-
-// A sequence's blocks are split into ceil(blocks / PART_BLOCKS) partitions of
-// near-equal size (so a 600-token context is 19 + 19 blocks, not 32 + 6).
-NIA_DEVICE void decode_partition(int ctx_blocks, int part_blocks, int part, int& nparts,
-                                 int& begin, int& end) {
-  nparts = (ctx_blocks + part_blocks - 1) / part_blocks;
-  begin = (int)(((int64_t)part * ctx_blocks) / nparts);
-  end = (int)(((int64_t)(part + 1) * ctx_blocks) / nparts);
-}
-
-// One work item: partition `part` (blocks [blk_begin, blk_end)) of sequence b and
-// KV head hk, all G query heads of the group, over a bf16 or an fp8 cache.  The
-// workgroup's 4 waves take the partition's block pairs round-robin; their states
-// merge through LDS and leave as the final output (single-partition sequence) or
-// as a partial for the partition merge.
-template <int G, int PART_BLOCKS, bool FP8>
-NIA_DEVICE void decode_item(const DecodeParams& p, int b, int hk, int part, int nparts,
-                            int blk_begin, int blk_end, int ctx) {
-  constexpr int D = 128;
-  using KR = typename KvRegs<FP8>::K;
-  using VR = typename KvRegs<FP8>::V;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int kc = lane & 7;     // K layout: 16-dim chunk
-  const int vrow = lane >> 4;  // V layout: token within a 4-token load
-  const int vc = lane & 15;    // V layout: 8-dim chunk
-
-  const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
-
-  // The partition's block-table slice, one entry per lane, read once so that
-  // no K/V load waits behind a table load inside the loop.
-  static_assert(PART_BLOCKS <= kWave, "one table entry per lane");
-  const int my_bt = (lane < blk_end - blk_begin) ? bt[blk_begin + lane] : -1;
-
-  DecodeState<G> st;
-  {
-    const bf16_t* qb = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)b * p.q_b;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const uint4* qp = reinterpret_cast<const uint4*>(qb + (int64_t)(hk * G + g) * p.q_h + 16 * kc);
-      const uint4 a = qp[0], c = qp[1];
-      st.qw[g][0] = a.x; st.qw[g][1] = a.y; st.qw[g][2] = a.z; st.qw[g][3] = a.w;
-      st.qw[g][4] = c.x; st.qw[g][5] = c.y; st.qw[g][6] = c.z; st.qw[g][7] = c.w;
-      st.m[g] = -INFINITY;
-      st.l[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) st.o[g][e] = 0.f;
-    }
-  }
-
-  {
-    constexpr int kStep = 2 * kDecodeWaves;
-    if constexpr (rolling_loop(G, FP8)) {
-      // Rolling pipeline: the next pair's K loads go out as soon as this pair's
-      // scores are taken, its V loads as soon as this pair's P V is issued, so a wave
-      // keeps loads in flight while it computes.
-      int jb = blk_begin + 2 * wave;
-      if (jb < blk_end) {
-        KR kA, kB;
-        VR vA, vB;
-        int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
-        int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
-        decode_load_k(p, bA, hk, lane, kA);
-        decode_load_v(p, bA, hk, lane, vA);
-        decode_load_k(p, bB, hk, lane, kB);
-        decode_load_v(p, bB, hk, lane, vB);
-        for (;;) {
-          float xs[2][2][G];
-          decode_qk_pair<G>(p, st, kA, kB, bA >= 0, bB >= 0, jb, ctx, lane, xs);
-          const int jn = jb + kStep;
-          const bool more = jn < blk_end;
-          int nA = -1, nB = -1;
-          // fp8: the v scales ride with K; keep this pair's until P V has used them.
-          KR kA2 = kA, kB2 = kB;
-          // The next pair's loads reuse this pair's registers: keep them behind the
-          // instructions that read those registers.
-          __builtin_amdgcn_sched_barrier(0);
-          if (more) {
-            nA = decode_block_id(p, my_bt, jn, blk_begin, blk_end);
-            nB = decode_block_id(p, my_bt, jn + 1, blk_begin, blk_end);
-            decode_load_k(p, nA, hk, lane, kA);
-            decode_load_k(p, nB, hk, lane, kB);
-          }
-          decode_pv_pair<G>(p, st, xs, kA2, kB2, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
-          if (!more) break;
-          __builtin_amdgcn_sched_barrier(0);
-          decode_load_v(p, nA, hk, lane, vA);
-          decode_load_v(p, nB, hk, lane, vB);
-          bA = nA;
-          bB = nB;
-          jb = jn;
-        }
-      }
-    } else {
-      for (int jb = blk_begin + 2 * wave; jb < blk_end; jb += kStep) {
-        KR kA, kB;
-        VR vA, vB;
-        const int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
-        const int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
-        decode_load_k(p, bA, hk, lane, kA);
-        decode_load_v(p, bA, hk, lane, vA);
-        decode_load_k(p, bB, hk, lane, kB);
-        decode_load_v(p, bB, hk, lane, vB);
-        float xs[2][2][G];
-        decode_qk_pair<G>(p, st, kA, kB, bA >= 0, bB >= 0, jb, ctx, lane, xs);
-        decode_pv_pair<G>(p, st, xs, kA, kB, vA, vB, bA >= 0, bB >= 0, jb, ctx, lane);
-      }
-    }
-  }
-
-  // ---- wave totals: rows of the V layout add (shared max); l counted 8x ----------------
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      st.o[g][e] += __shfl_xor(st.o[g][e], 16, kWave);
-      st.o[g][e] += __shfl_xor(st.o[g][e], 32, kWave);
-    }
-    st.l[g] = wave_sum(st.l[g]) * 0.125f;
-  }
-  merge_waves_and_store<bf16_t, D, G>(p, st.o, st.m, st.l, vrow, vc, wave, b, hk, part, nparts);
-}
-
-// ---- matrix-core block loop: batches of at most kDmaMaxBatch -------------------------------
-// The vector-unit loops spend ~100 G instructions per block pair and lane on q . k and
-// P V, which bounds large groups below the memory rate (Qwen2.5-VL, G = 7: 68.6 us here
-// against 59.7) and costs the Qwen3-8B batch (G = 4) 2%.  Here, per block of 16 keys:
-//   S^T = K Q^T: 4 v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims of K, B = Q^T with the
-//         group's heads in columns 0..G-1 and zeros beyond), then scale * log2 e in fp32;
-//   O^T += V^T P^T: 8 v_mfma_f32_16x16x16_bf16, one per 16-dim tile (A = V^T read from
-//         LDS with ds_read_b64_tr_b16, B = P^T, which is the S^T accumulator as it is).
-// In both accumulators lane l owns head l % 16 and rows 4 (l / 16) .. + 3 of the tile, so
-// a head's scores sit in lanes l, l ^ 16, l ^ 32, l ^ 48 and the O rescale is lane-local.
-// The block pairs stream through a 16 KB LDS slot per wave, [K A][V A][K B][V B]: the
-// next pair's DMA is issued as soon as this pair is read out, so a wave holds no
-// registers for loads in flight.  K is placed for its A operand (step j of lane l at
-// 1024 j + 16 l, one ds_read_b128), V row-major with 16-byte chunk c of row r at
-// c ^ tile_swz(r).
-constexpr int kDmaWaveBytes = 16384;
-// Largest batch of this kernel: its sequence index (4 KB) and the four slots (64 KB)
-// keep two workgroups per CU.
-constexpr int kDmaMaxBatch = 1024;
-constexpr bool staged_loop(int, bool) { return true; }
-
-struct MfmaLaneOffsets {
-  uint32_t k_src[4];  // DMA source offsets in a 4 KB block-head
-  uint32_t v_src[4];
-  int v_read[8];      // transposed read of 16-dim tile mt in the V part
-};
-
-NIA_DEVICE MfmaLaneOffsets mfma_lane_offsets(int lane) {
-  MfmaLaneOffsets o;
-  const int key = lane & 15, quad = lane >> 4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    // K: lane l of step j reads key l % 16, dims 32 j + 8 quad .. + 7
-    o.k_src[j] = (uint32_t)(key * 256 + 64 * j + 16 * quad);
-    // V: DMA j fills rows 4 j .. + 3; lane l writes row 4 j + quad at chunk position
-    // l % 16, which holds chunk (l % 16) ^ tile_swz(row)
-    const int r = 4 * j + quad;
-    o.v_src[j] = (uint32_t)(r * 256 + 16 * (key ^ tile_swz(r)));
-  }
-  // ds_read_b64_tr_b16 for the A operand (dim 16 mt + l % 16, keys 4 quad .. + 3): lane
-  // i = 4 rr + q of a 16-lane group addresses row 4 quad + rr, dims 16 mt + 4 q .. + 3.
-  const int i = lane & 15, rr = i >> 2, q = i & 3, row = 4 * quad + rr;
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt)
-    o.v_read[mt] = row * 256 + 16 * ((2 * mt + (q >> 1)) ^ tile_swz(row)) + 8 * (q & 1);
-  return o;
-}
-
-// DMA of block-head (blk, hk) of K and V into part (8 KB of a slot).  An invalid block
-// (blk < 0) issues nothing: its scores are masked and its V zeroed after the read.
-NIA_DEVICE void mfma_dma_block(const DecodeParams& p, int blk, int hk, const MfmaLaneOffsets& o,
-                               uint8_t* part) {
-  if (blk < 0) return;
-  // both are wave-uniform (a table entry read by readlane, the item's KV head); saying
-  // so keeps the resources in scalar registers without a waterfall loop
-  blk = uniform(blk);
-  hk = uniform(hk);
-  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)block_head(p.k_cache, p, blk, hk, 256), 0, 4096, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)block_head(p.v_cache, p, blk, hk, 256), 0, 4096, kBufferWord3);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) lds_dma16(kr, o.k_src[j], part + 1024 * j);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) lds_dma16(vr, o.v_src[j], part + 4096 + 1024 * j);
-}
-
-// fp8 caches: a block part (8 KB of the slot) holds [K codes 2 KB][V codes 2 KB][V bf16 4 KB].
-// K: DMA d of lane l brings key l % 16, codes of dims 64 d + 16 quad .. + 15, to 1024 d + 16 l;
-// they feed QK steps 2 d (first 8 dims) and 2 d + 1 (last 8), and Q is laid out the same way.
-// V: the codes are copied as they are; each lane widens 16 of them (row 8 d + l / 8, dims
-// 16 (l % 8) .. + 15) into the bf16 part, row-major with the chunk swizzle, for the transposed
-// reads of the bf16 loop.
-NIA_DEVICE void mfma_dma_block_fp8(const DecodeParams& p, int blk, int hk, int lane, uint8_t* part) {
-  if (blk < 0) return;
-  blk = uniform(blk);
-  hk = uniform(hk);
-  const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)block_head(p.k_cache, p, blk, hk, 128), 0, 2048, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)block_head(p.v_cache, p, blk, hk, 128), 0, 2048, kBufferWord3);
-  const uint32_t ksrc = (uint32_t)((lane & 15) * 128 + 16 * (lane >> 4));
-#pragma unroll
-  for (int d = 0; d < 2; ++d) lds_dma16(kr, ksrc + 64u * d, part + 1024 * d);
-#pragma unroll
-  for (int d = 0; d < 2; ++d) lds_dma16(vr, 16u * lane + 1024u * d, part + 2048 + 1024 * d);
-}
-
-// 8 e4m3 codes (two dwords) -> 8 bf16 (exact).
-NIA_DEVICE uint4 widen_fp8x8(uint32_t a, uint32_t b) {
-  return make_uint4(bf16x2_from_fp8x2<false>(a), bf16x2_from_fp8x2<true>(a),
-                    bf16x2_from_fp8x2<false>(b), bf16x2_from_fp8x2<true>(b));
-}
-
-template <int G, int PART_BLOCKS, bool FP8 = false>
-NIA_DEVICE void decode_item_mfma(const DecodeParams& p, int b, int hk, int part, int nparts,
-                                 int blk_begin, int blk_end, int ctx, uint8_t* dma_buf) {
-  constexpr int D = 128;
-  constexpr int BS = 16;
-  static_assert(G <= 16, "the group's heads fill columns of a 16-wide tile");
-  static_assert(PART_BLOCKS <= kWave, "one table entry per lane");
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = uniform(threadIdx.x / kWave);
-  const int hn = lane & 15;   // head of the group in this lane's accumulator column
-  const int quad = lane >> 4;
-  const int32_t* bt = p.block_tables + (int64_t)b * p.bt_stride;
-  const int my_bt = (lane < blk_end - blk_begin) ? bt[blk_begin + lane] : -1;
-
-  // B operand of S^T: head hn, dims 32 j + 8 quad .. + 7 (fp8: 64 (j / 2) + 16 quad + 8 (j % 2)
-  // .. + 7, the order of the K codes), as given: the scores leave the MFMAs as exact-product
-  // fp32 sums and take scale * log2(e) in fp32 (a bf16-rounded scaled Q would move each
-  // score by up to 2^-9 of its size)
-  uint4 qb[4];
-  {
-    const bf16_t* qp = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)b * p.q_b +
-                       (int64_t)(hk * G + (hn < G ? hn : 0)) * p.q_h;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d0 = FP8 ? 64 * (j >> 1) + 16 * quad + 8 * (j & 1) : 32 * j + 8 * quad;
-      qb[j] = hn < G ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
-    }
-  }
-  f32x4_t oacc[8];
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt) oacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // the head's running max (the same in its four lanes)
-  float l_run = 0.f;        // this lane's share of the head's sum
-
-  const MfmaLaneOffsets off = mfma_lane_offsets(lane);
-  uint8_t* slot = dma_buf + wave * kDmaWaveBytes;
-  constexpr int kStep = 2 * kDecodeWaves;
-  int jb = blk_begin + 2 * wave;
-  if (jb < blk_end) {
-    int bA = decode_block_id(p, my_bt, jb, blk_begin, blk_end);
-    int bB = decode_block_id(p, my_bt, jb + 1, blk_begin, blk_end);
-    // fp8: the row scales of the pair's keys 4 quad .. + 3 (zeros for an invalid block)
-    float4 ks[2], vs[2];
-    auto issue = [&](int x, int blk) __attribute__((always_inline)) {
-      if constexpr (FP8) {
-        mfma_dma_block_fp8(p, blk, hk, lane, slot + 8192 * x);
-        const int64_t row0 = ((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) * 16 + 4 * quad;
-        ks[x] = blk >= 0 ? *reinterpret_cast<const float4*>(p.k_scale + row0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        vs[x] = blk >= 0 ? *reinterpret_cast<const float4*>(p.v_scale + row0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      } else {
-        mfma_dma_block(p, blk, hk, off, slot + 8192 * x);
-      }
-    };
-    issue(0, bA);
-    issue(1, bB);
-    for (;;) {
-      __builtin_amdgcn_s_waitcnt(0);  // this pair is in the slot
-      uint4 ka[2][4];
-      s16x4_t va[2][8];
-      float4 ksc[2], vsc[2];  // this pair's scales (fp8)
-      if constexpr (FP8) {
-        // widen V into the bf16 parts (each wave its own slot: no barrier), K into registers
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          ksc[x] = ks[x];
-          vsc[x] = vs[x];
-#pragma unroll
-          for (int d = 0; d < 2; ++d) {
-            const uint4 kc = *reinterpret_cast<const uint4*>(slot + 8192 * x + 1024 * d + 16 * lane);
-            ka[x][2 * d] = widen_fp8x8(kc.x, kc.y);
-            ka[x][2 * d + 1] = widen_fp8x8(kc.z, kc.w);
-            const uint4 vc = *reinterpret_cast<const uint4*>(slot + 8192 * x + 2048 + 1024 * d + 16 * lane);
-            const int r = 8 * d + (lane >> 3), c = 2 * (lane & 7);
-            uint8_t* vrow = slot + 8192 * x + 4096 + r * 256;
-            *reinterpret_cast<uint4*>(vrow + 16 * (c ^ tile_swz(r))) = widen_fp8x8(vc.x, vc.y);
-            *reinterpret_cast<uint4*>(vrow + 16 * ((c + 1) ^ tile_swz(r))) = widen_fp8x8(vc.z, vc.w);
-          }
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // the widened V rows are in place
-      } else {
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            ka[x][j] = *reinterpret_cast<const uint4*>(slot + 8192 * x + 1024 * j + 16 * lane);
-      }
-#pragma unroll
-      for (int x = 0; x < 2; ++x)
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) va[x][mt] = lds_read_tr16(slot + 8192 * x + 4096 + off.v_read[mt]);
-      __builtin_amdgcn_s_waitcnt(0);  // read out before the slot is refilled
-      __builtin_amdgcn_sched_barrier(0);
-      const int jn = jb + kStep;
-      const bool more = jn < blk_end;
-      int nA = -1, nB = -1;
-      if (more) {
-        nA = decode_block_id(p, my_bt, jn, blk_begin, blk_end);
-        nB = decode_block_id(p, my_bt, jn + 1, blk_begin, blk_end);
-        issue(0, nA);
-        issue(1, nB);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-
-      // ---- scores, masked past the context and in invalid blocks ----------------------------
-      f32x4_t sc[2];
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        sc[x] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sc[x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[x][j]),
-                                                          __builtin_bit_cast(bf16x8_t, qb[j]),
-                                                          sc[x], 0, 0, 0);
-      }
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        if constexpr (FP8) {
-          sc[x][0] *= ksc[x].x * p.scale_log2;
-          sc[x][1] *= ksc[x].y * p.scale_log2;
-          sc[x][2] *= ksc[x].z * p.scale_log2;
-          sc[x][3] *= ksc[x].w * p.scale_log2;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sc[x][i] *= p.scale_log2;
-        }
-        const bool ok = x ? bB >= 0 : bA >= 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (!ok || (jb + x) * BS + 4 * quad + i >= ctx) sc[x][i] = -INFINITY;
-      }
-      // ---- lazy running max (raised when a P above 2^8 is possible) -------------------------
-      float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                       fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-      bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-      bm = fmaxf(bm, max_xor32(bm));
-      if (wave_any(bm > m_run + kLazyRescale)) {
-        const float mn = fmaxf(m_run, bm);
-        const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
-        m_run = mn;
-        l_run *= corr;
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) oacc[mt] *= corr;
-      }
-      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
-      // ---- P^T (keys 4 quad .. + 3 of each block) and O^T += V^T P^T ------------------------
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        // V of keys past the context or of an invalid block may be stale (any bits, NaN
-        // included), and 0 * NaN would poison O: zero them (and their fp8 row scales).
-        const bool ok = x ? bB >= 0 : bA >= 0;
-        const int key0 = (jb + x) * BS;
-        uint32_t p01, p23;
-        if constexpr (FP8) {
-          const int kq = key0 + 4 * quad;
-          const float e0 = fast_exp2(sc[x][0] - msub), e1 = fast_exp2(sc[x][1] - msub);
-          const float e2 = fast_exp2(sc[x][2] - msub), e3 = fast_exp2(sc[x][3] - msub);
-          l_run += (e0 + e1) + (e2 + e3);
-          // the weights that multiply the V codes carry the rows' v scales
-          p01 = pack_bf16x2(e0 * (ok && kq < ctx ? vsc[x].x : 0.f), e1 * (ok && kq + 1 < ctx ? vsc[x].y : 0.f));
-          p23 = pack_bf16x2(e2 * (ok && kq + 2 < ctx ? vsc[x].z : 0.f), e3 * (ok && kq + 3 < ctx ? vsc[x].w : 0.f));
-        } else {
-          p01 = pack_bf16x2(fast_exp2(sc[x][0] - msub), fast_exp2(sc[x][1] - msub));
-          p23 = pack_bf16x2(fast_exp2(sc[x][2] - msub), fast_exp2(sc[x][3] - msub));
-          l_run = dot2_bf16(p01, kBf16OnePair, l_run);
-          l_run = dot2_bf16(p23, kBf16OnePair, l_run);
-        }
-        const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(p01, p23));
-        if (!ok || key0 + BS > ctx) {
-          const int kq = key0 + 4 * quad;
-          const uint32_t m01 = (ok && kq < ctx ? 0xffffu : 0u) | (ok && kq + 1 < ctx ? 0xffff0000u : 0u);
-          const uint32_t m23 = (ok && kq + 2 < ctx ? 0xffffu : 0u) | (ok && kq + 3 < ctx ? 0xffff0000u : 0u);
-#pragma unroll
-          for (int mt = 0; mt < 8; ++mt) {
-            uint2 w = __builtin_bit_cast(uint2, va[x][mt]);
-            w.x &= m01;
-            w.y &= m23;
-            va[x][mt] = __builtin_bit_cast(s16x4_t, w);
-          }
-        }
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt)
-          oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[x][mt], pt, oacc[mt], 0, 0, 0);
-      }
-      if (!more) break;
-      bA = nA;
-      bB = nB;
-      jb = jn;
-    }
-  }
-
-  // ---- wave state to LDS (o rows in the wave's own slot, which holds no pending DMA) ------
-  l_run += __shfl_xor(l_run, 16, kWave);
-  l_run += __shfl_xor(l_run, 32, kWave);
-  __shared__ float sm_m[kDecodeWaves * G];
-  __shared__ float sm_l[kDecodeWaves * G];
-  float* sm_o = reinterpret_cast<float*>(dma_buf);
-  constexpr int kStride = kDmaWaveBytes / 4;
-  static_assert(G * D <= kStride, "a wave's o rows fit its slot");
-  if (hn < G) {
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-      *reinterpret_cast<f32x4_t*>(sm_o + wave * kStride + hn * D + 16 * mt + 4 * quad) = oacc[mt];
-    if (quad == 0) {
-      sm_m[wave * G + hn] = m_run;
-      sm_l[wave * G + hn] = l_run;
-    }
-  }
-  __syncthreads();
-  merge_lds_and_store<bf16_t, D, G, kStride>(p, sm_o, sm_m, sm_l, b, hk, part, nparts);
-}
-
-// Zero output rows of a sequence with no keys (all G heads of KV head hk).
-template <int G>
-NIA_DEVICE void decode_zero_output(const DecodeParams& p, int b, int hk) {
-  constexpr int D = 128;
-  bf16_t* ob = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b;
-  for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads)
-    ob[(int64_t)(hk * G + idx / D) * p.out_h + idx % D] = (bf16_t)0.f;
-}
-
-// Grid-per-partition variant: grid (max partitions, KV heads, sequences); the
-// partials are merged by paged_decode_combine_kernel.  Used when the batch is
-// too large for the persistent kernel's LDS index.
-template <int G, int PART_BLOCKS, bool FP8>
-__global__ __launch_bounds__(kDecodeThreads) void paged_decode_bf16_kernel(DecodeParams p) {
-  constexpr int BS = 16;
-  const int part = blockIdx.x;
-  const int hk = blockIdx.y;
-  const int b = blockIdx.z;
-  int64_t ctx64 = p.context_lens[b];
-  const int64_t cap = (int64_t)p.max_blocks * BS;
-  if (ctx64 > cap) ctx64 = cap;
-  const int ctx = ctx64 > 0 ? (int)ctx64 : 0;
-  int nparts, blk_begin, blk_end;
-  decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
-  if (part >= nparts) {
-    // Whole workgroup leaves together.  A sequence without keys gets zeros from
-    // its first partition.
-    if (part == 0 && ctx == 0) decode_zero_output<G>(p, b, hk);
-    return;
-  }
-  decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
-}
-
-// Largest batch the persistent kernel indexes in LDS (prefix sums of the
-// per-sequence partition counts).
-constexpr int kPersistentMaxBatch = 4096;
-
 // Inclusive prefix sum over the lanes of a wave.
 NIA_DEVICE int wave_inclusive_scan(int x, int lane) {
 #pragma unroll
@@ -1281,254 +516,664 @@ NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
   return base + inc - v;
 }
 
-// Persistent variant: a grid of as many workgroups as the chip holds at once.
-// Work items are (sequence, partition, KV head) in that order, numbered on the
-// device from context_lens; workgroup w starts with item w and then takes items
-// from an atomic ticket counter (the next ticket is requested while the current
-// item runs), so the grid never carries empty workgroups and a short item is
-// followed at once by the next.  Partials go to paged_decode_combine_kernel,
-// launched after this one.  The two counters live at the start of the
-// workspace: they must be zero before the first call, and the last workgroup to
-// leave returns them to zero.
-template <int G, int PART_BLOCKS, bool FP8, bool DMA = false>
-__global__ __launch_bounds__(kDecodeThreads)
-__attribute__((amdgpu_waves_per_eu(persistent_waves(G, FP8 && !DMA)))) void paged_decode_bf16_persistent_kernel(
-    DecodeParams p, int batch, int* counters) {
-  constexpr int BS = 16;
-  constexpr int kMaxBatch = DMA ? kDmaMaxBatch : kPersistentMaxBatch;
-  __shared__ int s_prefix[kMaxBatch + 1];  // first item number of each sequence
-  uint8_t* dma_buf = nullptr;
-  if constexpr (DMA) {
-    __shared__ __attribute__((aligned(1024))) uint8_t s_dma[kDecodeWaves * kDmaWaveBytes];
-    dma_buf = s_dma;
+// ---- key-range split decode (bf16 caches and the fp8 format) --------------------------------
+
+constexpr int kSlotBytes = 16384;      // a wave's LDS slot: [K tile 0][V tile 0][K tile 1][V tile 1]
+constexpr int kUnitKeys = 32;          // keys per unit (two 16-key tiles)
+constexpr int kSplitLdsBatch = 2048;   // batches whose unit prefix each workgroup builds in LDS
+constexpr int kSplitMaxGrid = 512;     // workgroups at most (sizes the partial slots)
+
+// 16-byte DMA global -> LDS with a wave-uniform byte offset (soffset) on top of the lane's.
+NIA_DEVICE void lds_dma16_s(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
+                            uint8_t* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16, voffset, (int)soffset, 0, 0);
+}
+
+// Per-lane offsets of the split kernel's tile traffic (bf16 rows, laid out for D = 128
+// whatever D is: 256-byte LDS rows, 16-byte chunk c of row r at position c ^ tile_swz(r)).
+template <int D>
+struct SplitLane {
+  uint32_t src[4];  // DMA j (rows 4 j .. + 3): the lane's bytes from row 4 j of the tile
+  bool dma_ok[4];   // its chunk lies inside the D-wide row
+  int k_read[4];    // K operand of QK step s (32 dims): row l % 16, chunk 4 s + l / 16
+  int k_tail;       // K operand of the last 16-dim step when D % 32 == 16
+  int v_read[8];    // transposed V read (ds_read_b64_tr_b16) of 16-dim tile mt
+};
+
+template <int D>
+NIA_DEVICE SplitLane<D> split_lane(int lane) {
+  SplitLane<D> o;
+  const int pos = lane & 15, quad = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // DMA j writes lane l's 16 bytes at row 4 j + l / 16, chunk position l % 16, which
+    // holds chunk (l % 16) ^ tile_swz(row)
+    const int r = 4 * j + quad;
+    const int c = pos ^ tile_swz(r);
+    o.dma_ok[j] = c < D / 8;
+    o.src[j] = (uint32_t)((quad * D + 8 * c) * 2);
+    o.k_read[j] = pos * 256 + 16 * ((4 * j + quad) ^ tile_swz(pos));
   }
+  o.k_tail = pos * 256 + 16 * ((D / 8 - 2 + (quad >> 1)) ^ tile_swz(pos)) + 8 * (quad & 1);
+  // ds_read_b64_tr_b16 for the A operand (dim 16 mt + l % 16, keys 4 quad .. + 3): lane
+  // i = 4 rr + q of a 16-lane group addresses row 4 quad + rr, dims 16 mt + 4 q .. + 3.
+  const int i = lane & 15, rr = i >> 2, q = i & 3, row = 4 * quad + rr;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+    o.v_read[mt] = row * 256 + 16 * ((2 * mt + (q >> 1)) ^ tile_swz(row)) + 8 * (q & 1);
+  return o;
+}
+
+// 8 e4m3 codes (two dwords) -> 8 bf16 (exact).
+NIA_DEVICE uint4 widen_fp8x8(uint32_t a, uint32_t b) {
+  return make_uint4(bf16x2_from_fp8x2<false>(a), bf16x2_from_fp8x2<true>(a),
+                    bf16x2_from_fp8x2<false>(b), bf16x2_from_fp8x2<true>(b));
+}
+
+// One wave's position in the unit stream: unit u of head group g, pair j of sequence b.
+struct SplitUnit {
+  int64_t u;   // -1: past the wave's range
+  int64_t U0;  // first unit of (g, b)
+  int b, g, j, n, ctx;  // n: units of sequence b; ctx: its context length (clamped)
+};
+
+template <int D, bool FP8>
+__global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeParams p,
+                                                                         int batch) {
+  static_assert(!FP8 || D == 128, "fp8 caches hold 128-dim rows");
+  static_assert(D % 16 == 0 && D >= 64 && D <= 128, "head_dim 64 .. 128, a multiple of 16");
+  constexpr int kSteps = D / 32;          // QK steps of 32 dims
+  constexpr bool kTail = D % 32 != 0;     // and one of 16 dims
+  constexpr int kDt = D / 16;             // PV tiles of 16 dims
+  __shared__ __attribute__((aligned(1024))) uint8_t s_dma[kDecodeWaves * kSlotBytes];
+  __shared__ int s_pfx[kSplitLdsBatch + 1];
   __shared__ int s_wave[kDecodeWaves];
-  __shared__ int s_ticket[2];
   const int tid = threadIdx.x;
-  const int64_t cap = (int64_t)p.max_blocks * BS;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int hn = lane & 15;    // query head of the group in this lane's accumulator column
+  const int quad = lane >> 4;  // rows (keys / dims) 4 quad .. + 3 of the accumulators
+  const int bs_log2 = p.bs_log2;
+  const int bs_mask = (1 << bs_log2) - 1;
+  const int64_t cap = (int64_t)p.max_blocks << bs_log2;
+  const int G = p.group;
 
-  // The first item is the workgroup's own id; later tickets come from the counter,
-  // offset by the grid size.  (All workgroups asking one counter at launch would
-  // queue on it for several microseconds before any KV load.)
-  if (tid == 0) s_ticket[0] = blockIdx.x;
-
-  // ---- work index -------------------------------------------------------------------------
-  // Thread t owns sequences [t * kPer, t * kPer + kPer): their context lengths are
-  // loaded together, once, and a workgroup scan of the partition counts gives each
-  // sequence's first item number.
-  constexpr int kPer = (kMaxBatch + kDecodeThreads - 1) / kDecodeThreads;
-  const int b0 = tid * kPer;
-  int nparts[kPer];
-  int run = 0;
+  // ---- units before each sequence (one head group) ----------------------------------------
+  const int* pfx = p.ws_pfx;  // large batches: written by decode_prefix_kernel
+  if (batch <= kSplitLdsBatch) {
+    constexpr int kPer = kSplitLdsBatch / kDecodeThreads;
+    const int b0 = tid * kPer;
+    int units[kPer];
+    int run = 0;
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    int64_t c = b0 + k < batch ? p.context_lens[b0 + k] : 0;
-    c = c < 0 ? 0 : (c > cap ? cap : c);
-    const int blocks = (int)((c + BS - 1) / BS);
-    // a sequence without keys is one item (it writes the zero output)
-    nparts[k] = b0 + k < batch ? (blocks > 0 ? (blocks + PART_BLOCKS - 1) / PART_BLOCKS : 1) : 0;
-    run += nparts[k];
-  }
-  int seq_items = 0;
-  int base = block_exclusive_scan(run, s_wave, seq_items);
+    for (int k = 0; k < kPer; ++k) {
+      int64_t c = b0 + k < batch ? p.context_lens[b0 + k] : 0;
+      c = c < 0 ? 0 : (c > cap ? cap : c);
+      units[k] = (int)((c + kUnitKeys - 1) / kUnitKeys);
+      run += units[k];
+    }
+    int tot = 0;
+    int base = block_exclusive_scan(run, s_wave, tot);
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    if (b0 + k < batch) s_prefix[b0 + k] = base;
-    base += nparts[k];
+    for (int k = 0; k < kPer; ++k) {
+      if (b0 + k < batch) s_pfx[b0 + k] = base;
+      base += units[k];
+    }
+    if (tid == 0) s_pfx[batch] = tot;
+    __syncthreads();
+    if (blockIdx.x == 0)  // for the combine kernel
+      for (int i = tid; i <= batch; i += kDecodeThreads) p.ws_pfx[i] = s_pfx[i];
+    pfx = s_pfx;
   }
-  if (tid == 0) s_prefix[batch] = seq_items;
-  __syncthreads();
-  const int total = seq_items * p.num_kv_heads;
+  const int T = uniform(pfx[batch]);
+  const int64_t total = (int64_t)T * p.nhg;
+  const int hg = p.hg, wph = p.wph;
+  const int hig = wave % hg;   // KV head within the group
+  const int slice = wave / hg;
+  const int64_t nv = (int64_t)p.grid * wph;
+  const int64_t vw = (int64_t)blockIdx.x * wph + slice;
+  const int64_t ustart = total * vw / nv;
+  const int64_t uend = total * (vw + 1) / nv;
+  if (ustart >= uend) return;  // no barrier follows: waves leave on their own
 
-  // ---- item loop ------------------------------------------------------------------------
-  for (int it = 0;; ++it) {
-    const int item = s_ticket[it & 1];
-    if (item >= total) break;
-    // Ask for the next ticket now; its value is only needed at the end of this
-    // item, so the request's latency hides behind the item's loads.
-    int next = 0;
-    if (tid == 0) next = (int)gridDim.x + atomicAdd(&counters[0], 1);
-    const int sp = item / p.num_kv_heads;
-    const int hk = item - sp * p.num_kv_heads;
-    int lo = 0, hi = batch;  // largest b with s_prefix[b] <= sp
+  // ---- walking the unit range ----------------------------------------------------------------
+  auto locate = [&](int64_t u, SplitUnit& x) __attribute__((always_inline)) {
+    x.u = u;
+    x.g = (int)(u / T);
+    const int r = (int)(u - (int64_t)x.g * T);
+    int lo = 0, hi = batch;  // pfx[lo] <= r < pfx[hi]; ends on the sequence holding r
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (s_prefix[mid] <= sp) lo = mid; else hi = mid;
+      if (pfx[mid] <= r) lo = mid; else hi = mid;
     }
-    const int b = lo;
-    const int part = sp - s_prefix[b];
-    int64_t c = p.context_lens[b];
+    x.b = uniform(lo);
+    const int p0 = uniform(pfx[x.b]);
+    x.j = r - p0;
+    x.n = uniform(pfx[x.b + 1]) - p0;
+    x.U0 = (int64_t)x.g * T + p0;
+    int64_t c = p.context_lens[x.b];
     c = c < 0 ? 0 : (c > cap ? cap : c);
-    const int ctx = (int)c;
-    if (ctx == 0) {
-      decode_zero_output<G>(p, b, hk);
+    x.ctx = uniform((int)c);
+  };
+  auto advance = [&](SplitUnit& x) __attribute__((always_inline)) {
+    if (x.u < 0) return;
+    if (x.u + 1 >= uend) {
+      x.u = -1;
+      return;
+    }
+    if (x.j + 1 < x.n) {
+      ++x.u;
+      ++x.j;
     } else {
-      int nparts, blk_begin, blk_end;
-      decode_partition((ctx + BS - 1) / BS, PART_BLOCKS, part, nparts, blk_begin, blk_end);
-      if constexpr (DMA)
-        decode_item_mfma<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx,
-                                              dma_buf);
-      else
-        decode_item<G, PART_BLOCKS, FP8>(p, b, hk, part, nparts, blk_begin, blk_end, ctx);
+      locate(x.u + 1, x);
     }
-    if (tid == 0) s_ticket[(it + 1) & 1] = next;
-    __syncthreads();  // next ticket visible; LDS of this item free
-  }
-  // ---- leave: the last workgroup out returns the counters to zero -------------------------
-  // Every workgroup increments the exit count only after its final (failed)
-  // ticket request returned, so when the count completes no request is pending.
-  if (tid == 0) {
-    const int left = atomicAdd(&counters[1], 1);
-    if (left == (int)gridDim.x - 1) {
-      atomicExch(&counters[0], 0);
-      atomicExch(&counters[1], 0);
+  };
+  // Lanes 0 .. 7: the blocks of a unit's 32 keys, (32 j >> bs_log2) + lane; -1 past the
+  // context, past the unit or for an id outside [0, num_blocks).
+  auto load_ids = [&](const SplitUnit& x) __attribute__((always_inline)) -> int {
+    if (x.u < 0) return -1;
+    const int k0 = kUnitKeys * x.j;
+    const int bi = (k0 >> bs_log2) + lane;
+    const int last = (min(k0 + kUnitKeys, x.ctx) - 1) >> bs_log2;
+    int id = -1;
+    if (lane < 8 && bi <= last) {
+      id = p.block_tables[(int64_t)x.b * p.bt_stride + bi];
+      if (id < 0 || (int64_t)id >= p.num_blocks) id = -1;
     }
+    return id;
+  };
+
+  const SplitLane<D> off = split_lane<D>(lane);
+  uint8_t* slot = s_dma + wave * kSlotBytes;
+  float4 ks[2], vs[2];  // fp8: row scales of the keys 4 quad .. + 3 of each tile in flight
+
+  // DMA of unit x's two tiles (KV head hk) into the slot.  Groups of 4 rows past the
+  // context or in an invalid block issue nothing; their keys are masked after the read.
+  auto issue = [&](const SplitUnit& x, int ids, int hk) __attribute__((always_inline)) {
+    const int k0 = kUnitKeys * x.j;
+    const int bi0 = k0 >> bs_log2;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      uint8_t* part = slot + 8192 * t;
+      if constexpr (FP8) {
+        // a tile lies in one block (block size >= 16)
+        const int key = k0 + 16 * t;
+        const int blk = key < x.ctx ? __builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0) : -1;
+        // the scales are read for every tile (block 0's rows stand in for a missing block)
+        // and zeroed after the read
+        const int64_t head = ((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << bs_log2;
+        const int64_t row0 = head + (key & bs_mask) + 4 * quad;
+        const float4 kq = *reinterpret_cast<const float4*>(p.k_scale + row0);
+        const float4 vq = *reinterpret_cast<const float4*>(p.v_scale + row0);
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        ks[t] = blk >= 0 ? kq : z;
+        vs[t] = blk >= 0 ? vq : z;
+        if (blk >= 0) {
+          const uint8_t* kb = reinterpret_cast<const uint8_t*>(p.k_cache) + head * 128;
+          const uint8_t* vb = reinterpret_cast<const uint8_t*>(p.v_cache) + head * 128;
+          const int bytes = 128 << bs_log2;
+          const __amdgpu_buffer_rsrc_t kr =
+              __builtin_amdgcn_make_buffer_rsrc((void*)kb, 0, bytes, kBufferWord3);
+          const __amdgpu_buffer_rsrc_t vr =
+              __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, bytes, kBufferWord3);
+          const uint32_t soff = (uint32_t)(key & bs_mask) * 128u;
+          // K: DMA d of lane l brings key l % 16, codes of dims 64 d + 16 quad .. + 15, to
+          // 1024 d + 16 l (the A operand order); V: the codes as they are (rows 8 d + l / 8)
+          const uint32_t ksrc = (uint32_t)(hn * 128 + 16 * quad);
+#pragma unroll
+          for (int d = 0; d < 2; ++d) lds_dma16_s(kr, ksrc + 64u * d, soff, part + 1024 * d);
+#pragma unroll
+          for (int d = 0; d < 2; ++d)
+            lds_dma16_s(vr, 16u * lane + 1024u * d, soff, part + 2048 + 1024 * d);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = k0 + 16 * t + 4 * j;  // rows 4 j .. + 3 lie in one block (>= 4 rows)
+          const int blk = key < x.ctx ? __builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0) : -1;
+          if (blk >= 0) {
+            const int64_t head = ((int64_t)blk * p.num_kv_heads + hk) << bs_log2;
+            const int bytes = (D * 2) << bs_log2;
+            const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(reinterpret_cast<const bf16_t*>(p.k_cache) + head * D), 0, bytes,
+                kBufferWord3);
+            const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(reinterpret_cast<const bf16_t*>(p.v_cache) + head * D), 0, bytes,
+                kBufferWord3);
+            const uint32_t soff = (uint32_t)((key & bs_mask) * D * 2);
+            if (off.dma_ok[j]) {
+              lds_dma16_s(kr, off.src[j], soff, part + 1024 * j);
+              lds_dma16_s(vr, off.src[j], soff, part + 4096 + 1024 * j);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  // B operand of S^T: head hn of the group, as given (the raw scores take scale * log2 e in
+  // fp32); dims 32 s + 8 quad .. + 7 (fp8: 64 (s / 2) + 16 quad + 8 (s % 2) .. + 7, the order
+  // of the K codes); the tail step dims D - 16 + 4 quad .. + 3.
+  auto load_q = [&](const SplitUnit& x, uint4 (&qv)[4], uint2& qt) __attribute__((always_inline)) {
+    const int hk = x.g * hg + hig;
+    const bf16_t* qp = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)x.b * p.q_b +
+                       (int64_t)(hk * G + (hn < G ? hn : 0)) * p.q_h;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int d0 = FP8 ? 64 * (s >> 1) + 16 * quad + 8 * (s & 1) : 32 * s + 8 * quad;
+      qv[s] = hn < G ? *reinterpret_cast<const uint4*>(qp + d0) : make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (kTail)
+      qt = hn < G ? *reinterpret_cast<const uint2*>(qp + D - 16 + 4 * quad) : make_uint2(0, 0);
+  };
+
+  f32x4_t oacc[kDt];
+#pragma unroll
+  for (int mt = 0; mt < kDt; ++mt) oacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // the head's running max (the same in its four lanes)
+  float l_run = 0.f;        // this lane's share of the head's sum
+
+  // Output of a finished sequence (the whole of it was this wave's), or the partial of
+  // the first / last sequence of the range (slot 0 / 1) for the combine kernel.
+  auto flush = [&](const SplitUnit& x) __attribute__((always_inline)) {
+    float ls = l_run + __shfl_xor(l_run, 16, kWave);
+    ls += __shfl_xor(ls, 32, kWave);
+    const int hk = x.g * hg + hig;
+    const bool whole = x.U0 >= ustart && x.U0 + x.n <= uend;
+    if (hn < G) {
+      if (whole) {
+        bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)x.b * p.out_b +
+                      (int64_t)(hk * G + hn) * p.out_h + 4 * quad;
+        const float inv = ls > 0.f ? 1.f / ls : 0.f;
+#pragma unroll
+        for (int mt = 0; mt < kDt; ++mt)
+          *reinterpret_cast<uint2*>(out + 16 * mt) =
+              make_uint2(pack_bf16x2(oacc[mt][0] * inv, oacc[mt][1] * inv),
+                         pack_bf16x2(oacc[mt][2] * inv, oacc[mt][3] * inv));
+      } else {
+        const int sl = x.U0 <= ustart ? 0 : 1;
+        const int64_t row = ((vw * 2 + sl) * hg + hig) * G + hn;
+        float* po = p.sp_o + row * D + 4 * quad;
+#pragma unroll
+        for (int mt = 0; mt < kDt; ++mt) *reinterpret_cast<f32x4_t*>(po + 16 * mt) = oacc[mt];
+        if (quad == 0) *reinterpret_cast<float2*>(p.sp_ml + 2 * row) = make_float2(m_run, ls);
+      }
+    }
+  };
+
+  // ---- pipeline: the unit in the slot (cur), the next one's DMA (n1), the table ids of the
+  // one after (n2) ------------------------------------------------------------------------------
+  SplitUnit cur, n1, n2;
+  locate(ustart, cur);
+  n1 = cur;
+  advance(n1);
+  n2 = n1;
+  advance(n2);
+  int ids_c = load_ids(cur);
+  int ids_1 = load_ids(n1);
+  uint4 qb[4], qn[4];
+  uint2 qt = make_uint2(0, 0), qnt = make_uint2(0, 0);
+  load_q(cur, qb, qt);
+  issue(cur, ids_c, cur.g * hg + hig);
+  for (;;) {
+    __builtin_amdgcn_s_waitcnt(0);  // this unit's tiles are in the slot
+    uint4 ka[2][4];
+    s16x4_t kta[2];
+    s16x4_t va[2][kDt];
+    float4 ksc[2], vsc[2];  // this unit's scales (fp8)
+    if constexpr (FP8) {
+      // widen V into the bf16 part of each tile (the wave's own slot: no barrier), K into
+      // registers
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        ksc[t] = ks[t];
+        vsc[t] = vs[t];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const uint4 kc = *reinterpret_cast<const uint4*>(slot + 8192 * t + 1024 * d + 16 * lane);
+          ka[t][2 * d] = widen_fp8x8(kc.x, kc.y);
+          ka[t][2 * d + 1] = widen_fp8x8(kc.z, kc.w);
+          const uint4 vc =
+              *reinterpret_cast<const uint4*>(slot + 8192 * t + 2048 + 1024 * d + 16 * lane);
+          const int r = 8 * d + (lane >> 3), c = 2 * (lane & 7);
+          uint8_t* vrow = slot + 8192 * t + 4096 + r * 256;
+          *reinterpret_cast<uint4*>(vrow + 16 * (c ^ tile_swz(r))) = widen_fp8x8(vc.x, vc.y);
+          *reinterpret_cast<uint4*>(vrow + 16 * ((c + 1) ^ tile_swz(r))) = widen_fp8x8(vc.z, vc.w);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // the widened V rows are in place
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s)
+          ka[t][s] = *reinterpret_cast<const uint4*>(slot + 8192 * t + off.k_read[s]);
+        if constexpr (kTail)
+          kta[t] = *reinterpret_cast<const s16x4_t*>(slot + 8192 * t + off.k_tail);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int mt = 0; mt < kDt; ++mt)
+        va[t][mt] = lds_read_tr16(slot + 8192 * t + 4096 + off.v_read[mt]);
+    __builtin_amdgcn_s_waitcnt(0);  // read out before the slot is refilled
+    __builtin_amdgcn_sched_barrier(0);
+    const bool new_seg = n1.u < 0 || n1.U0 != cur.U0;
+    if (n1.u >= 0) {
+      if (new_seg) load_q(n1, qn, qnt);
+      issue(n1, ids_1, n1.g * hg + hig);
+    }
+    const int ids_2 = load_ids(n2);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- scores, masked past the context and in invalid blocks ------------------------------
+    const int k0 = kUnitKeys * cur.j;
+    const int bi0 = k0 >> bs_log2;
+    const uint32_t okmask = (uint32_t)__builtin_amdgcn_ballot_w64(ids_c >= 0) & 0xffu;
+    bool blk_ok[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      blk_ok[t] = (okmask >> (((k0 + 16 * t + 4 * quad) >> bs_log2) - bi0)) & 1u;
+    f32x4_t sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[t][s]),
+                                                        __builtin_bit_cast(bf16x8_t, qb[s]),
+                                                        sc[t], 0, 0, 0);
+      if constexpr (kTail)
+        sc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+            kta[t], __builtin_bit_cast(s16x4_t, qt), sc[t], 0, 0, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if constexpr (FP8) {
+        sc[t][0] *= ksc[t].x * p.scale_log2;
+        sc[t][1] *= ksc[t].y * p.scale_log2;
+        sc[t][2] *= ksc[t].z * p.scale_log2;
+        sc[t][3] *= ksc[t].w * p.scale_log2;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[t][i] *= p.scale_log2;
+      }
+      const int kq = k0 + 16 * t + 4 * quad;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!blk_ok[t] || kq + i >= cur.ctx) sc[t][i] = -INFINITY;
+    }
+    // ---- lazy running max (raised when a P above 2^8 is possible) ---------------------------
+    float bm = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                     fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+    bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+    bm = fmaxf(bm, max_xor32(bm));
+    if (wave_any(bm > m_run + kLazyRescale)) {
+      const float mn = fmaxf(m_run, bm);
+      const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
+      m_run = mn;
+      l_run *= corr;
+#pragma unroll
+      for (int mt = 0; mt < kDt; ++mt) oacc[mt] *= corr;
+    }
+    const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+    // ---- P^T (keys 4 quad .. + 3 of each tile) and O^T += V^T P^T -----------------------------
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      // V of keys past the context or of an invalid block may be stale (any bits, NaN
+      // included), and 0 * NaN would poison O: zero them (and their fp8 row scales).
+      const int kq = k0 + 16 * t + 4 * quad;
+      const bool okq0 = blk_ok[t] && kq < cur.ctx, okq1 = blk_ok[t] && kq + 1 < cur.ctx;
+      const bool okq2 = blk_ok[t] && kq + 2 < cur.ctx, okq3 = blk_ok[t] && kq + 3 < cur.ctx;
+      uint32_t p01, p23;
+      if constexpr (FP8) {
+        const float e0 = fast_exp2(sc[t][0] - msub), e1 = fast_exp2(sc[t][1] - msub);
+        const float e2 = fast_exp2(sc[t][2] - msub), e3 = fast_exp2(sc[t][3] - msub);
+        l_run += (e0 + e1) + (e2 + e3);
+        // the weights that multiply the V codes carry the rows' v scales
+        p01 = pack_bf16x2(e0 * (okq0 ? vsc[t].x : 0.f), e1 * (okq1 ? vsc[t].y : 0.f));
+        p23 = pack_bf16x2(e2 * (okq2 ? vsc[t].z : 0.f), e3 * (okq3 ? vsc[t].w : 0.f));
+      } else {
+        p01 = pack_bf16x2(fast_exp2(sc[t][0] - msub), fast_exp2(sc[t][1] - msub));
+        p23 = pack_bf16x2(fast_exp2(sc[t][2] - msub), fast_exp2(sc[t][3] - msub));
+        l_run = dot2_bf16(p01, kBf16OnePair, l_run);
+        l_run = dot2_bf16(p23, kBf16OnePair, l_run);
+      }
+      const s16x4_t pt = __builtin_bit_cast(s16x4_t, make_uint2(p01, p23));
+      if (!(okq0 && okq3)) {
+        const uint32_t m01 = (okq0 ? 0xffffu : 0u) | (okq1 ? 0xffff0000u : 0u);
+        const uint32_t m23 = (okq2 ? 0xffffu : 0u) | (okq3 ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int mt = 0; mt < kDt; ++mt) {
+          uint2 w = __builtin_bit_cast(uint2, va[t][mt]);
+          w.x &= m01;
+          w.y &= m23;
+          va[t][mt] = __builtin_bit_cast(s16x4_t, w);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < kDt; ++mt)
+        oacc[mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[t][mt], pt, oacc[mt], 0, 0, 0);
+    }
+
+    if (new_seg) {
+      flush(cur);
+      m_run = -INFINITY;
+      l_run = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < kDt; ++mt) oacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qb[s] = qn[s];
+      qt = qnt;
+    }
+    if (n1.u < 0) break;
+    cur = n1;
+    n1 = n2;
+    advance(n2);
+    ids_c = ids_1;
+    ids_1 = ids_2;
   }
 }
 
-constexpr int kPartBlocks = 32;  // 512 tokens per work item at block size 16
-// Longer items when the batch holds at least kLongItemsPerWg of them per persistent
-// workgroup (counted from the block-table width, an upper bound): each item carries a
-// fixed cost (index lookup, table slice, the first loads' latency, the merge of the
-// waves), and with many items per workgroup the longer tail costs less than it saves
-// (Qwen3-8B decode 209 -> 207 us, its fp8 cache 141 -> 135 us; the Qwen2.5-VL batch,
-// about two items per workgroup, keeps 32).
-constexpr int kPartBlocksLong = 48;
-constexpr int kLongItemsPerWg = 6;
+// Units before each sequence into ws_pfx, for batches whose prefix does not fit the split
+// kernel's LDS (one workgroup, a running scan over chunks of the batch).
+__global__ __launch_bounds__(kDecodeThreads) void decode_prefix_kernel(DecodeParams p, int batch) {
+  __shared__ int s_wave[kDecodeWaves];
+  const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+  int base = 0;
+  for (int c0 = 0; c0 < batch; c0 += kDecodeThreads) {
+    const int b = c0 + (int)threadIdx.x;
+    int64_t c = b < batch ? p.context_lens[b] : 0;
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    const int u = (int)((c + kUnitKeys - 1) / kUnitKeys);
+    int tot = 0;
+    const int ex = block_exclusive_scan(u, s_wave, tot);
+    if (b < batch) p.ws_pfx[b] = base + ex;
+    base += tot;
+  }
+  if (threadIdx.x == 0) p.ws_pfx[batch] = base;
+}
 
-// Workspace layout: [work counters (256 B)][m, l per partial][o per partial].
-constexpr size_t kCounterBytes = 256;
+// Merge the partials of every (sequence, head) whose units were split over several waves'
+// ranges: one wave per pair.  Lane i takes the (m, l) of partial i (64 at a time), the
+// wave reduces the max and the weights, and each lane accumulates output dims lane,
+// lane + 64 over the partial rows, four rows per round of loads.  Pairs of empty
+// sequences get zeros; pairs finished by the split kernel are left alone.
+template <int D>
+__global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(DecodeParams p,
+                                                                               int batch) {
+  constexpr int DL = (D + kWave - 1) / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int pair = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6);
+  if (pair >= batch * p.num_heads) return;
+  const int b = pair / p.num_heads;
+  const int h = pair - b * p.num_heads;
+  const int G = p.group;
+  const int hk = h / G, gq = h - hk * G;
+  const int g = hk / p.hg, hig = hk - g * p.hg;
+  const int T = p.ws_pfx[batch];
+  const int pb = p.ws_pfx[b];
+  const int n_units = p.ws_pfx[b + 1] - pb;
+  bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h;
+  if (n_units <= 0) {
+    for (int d = lane; d < D; d += kWave) out[d] = (bf16_t)0.f;
+    return;
+  }
+  const int64_t total = (int64_t)T * p.nhg;
+  const int64_t nv = (int64_t)p.grid * p.wph;
+  const int64_t U0 = (int64_t)g * T + pb, U1 = U0 + n_units;
+  // the range holding unit u is the last vw with total * vw / nv <= u
+  const int64_t f = ((U0 + 1) * nv - 1) / total, e = (U1 * nv - 1) / total;
+  if (f == e) return;  // one wave had the whole sequence and wrote it
+  const int n = (int)(e - f + 1);
+  auto row_of = [&](int i, bool& live) -> int64_t {
+    const int64_t v = f + i;
+    const int64_t s0 = total * v / nv, s1 = total * (v + 1) / nv;
+    live = s0 < s1;  // an empty range wrote nothing
+    const int sl = U0 <= s0 ? 0 : 1;
+    return ((v * 2 + sl) * p.hg + hig) * G + gq;
+  };
+  float mt = -INFINITY;
+  for (int c0 = 0; c0 < n; c0 += kWave) {
+    bool live = false;
+    const int64_t row = c0 + lane < n ? row_of(c0 + lane, live) : 0;
+    if (live) mt = fmaxf(mt, p.sp_ml[2 * row]);
+  }
+  mt = wave_max(mt);
+  float ls = 0.f;
+  float acc[DL];
+#pragma unroll
+  for (int k = 0; k < DL; ++k) acc[k] = 0.f;
+  for (int c0 = 0; c0 < n; c0 += kWave) {
+    bool live = false;
+    const int64_t row = c0 + lane < n ? row_of(c0 + lane, live) : 0;
+    float w = 0.f;
+    if (live) {
+      const float2 ml = *reinterpret_cast<const float2*>(p.sp_ml + 2 * row);
+      w = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - mt);
+      ls = fmaf(ml.y, w, ls);
+    }
+    const int cnt = min(kWave, n - c0);
+    for (int j0 = 0; j0 < cnt; j0 += 4) {
+      float r[4][DL];
+      float wj[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int src = (j0 + jj) & (kWave - 1);
+        wj[jj] = j0 + jj < cnt ? __shfl(w, src, kWave) : 0.f;
+        const int64_t rj = __shfl(row, src, kWave);
+#pragma unroll
+        for (int k = 0; k < DL; ++k) {
+          const int d = lane + kWave * k;
+          // rows of ranges that saw no key hold no data: weight 0 and not read
+          r[jj][k] = (wj[jj] > 0.f && d < D) ? p.sp_o[rj * D + d] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int k = 0; k < DL; ++k) acc[k] = fmaf(r[jj][k], wj[jj], acc[k]);
+    }
+  }
+  ls = wave_sum(ls);
+  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+#pragma unroll
+  for (int k = 0; k < DL; ++k) {
+    const int d = lane + kWave * k;
+    if (d < D) out[d] = (bf16_t)(acc[k] * inv);
+  }
+}
+
+constexpr int kPartBlocks = 32;  // fp32 partition kernel: 512 tokens per partition
+
+// Workspace layout: [header (256 B)][per path:
+//   split:  ws_pfx (batch + 1 ints, rounded to 256 B)][sp_ml][sp_o]
+//   fp32 partitions:  [ws_ml][ws_o]]
+constexpr size_t kHeaderBytes = 256;
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-int32_t decode_max_parts(int32_t max_blocks_per_seq, int part_blocks = kPartBlocks) {
-  return (max_blocks_per_seq + part_blocks - 1) / part_blocks;
+int32_t decode_max_parts(int32_t max_blocks_per_seq) {
+  return (max_blocks_per_seq + kPartBlocks - 1) / kPartBlocks;
 }
 
-// Workgroups per CU the persistent kernel reaches, cached per (device, G).
+size_t split_pfx_bytes(int32_t batch) { return round_up((size_t)(batch + 1) * sizeof(int), 256); }
+
+// Partial rows of the split kernel: grid * wph ranges x 2 slots x hg heads x G = 8 G per
+// workgroup, for the largest grid.
+size_t split_rows(int32_t group) { return (size_t)kSplitMaxGrid * 8 * (size_t)group; }
+
+size_t split_workspace(int32_t batch, int32_t group, int32_t head_dim) {
+  return kHeaderBytes + split_pfx_bytes(batch) +
+         split_rows(group) * ((size_t)head_dim + 2) * sizeof(float);
+}
+
+bool split_shape(bool fp8, int32_t head_dim, int32_t block_size, int32_t group) {
+  const bool pow2 = block_size > 0 && (block_size & (block_size - 1)) == 0;
+  if (!pow2 || block_size < (fp8 ? 16 : 4) || group < 1 || group > 16) return false;
+  return fp8 ? head_dim == 128
+             : (head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128);
+}
+
+bool f32_partition_shape(int32_t head_dim, int32_t block_size, int32_t group) {
+  return head_dim == 128 && block_size == 16 && group <= 8;
+}
+
+// Workgroups of the split kernel: as many as the chip holds at once (two per CU, 8 waves),
+// cached per (device, kernel).
 std::mutex g_occ_mutex;
 std::map<std::pair<int, int>, int> g_occ;
 
-template <int G, bool FP8, int PB, bool DMA = false>
-int persistent_grid(int device, int upper) {
-  int per_cu = 0, cus = 0;
-  const int key = 8 * G + (DMA ? 4 : 0) + (PB == kPartBlocks ? 0 : 2) + (FP8 ? 1 : 0);
+template <int D, bool FP8>
+int split_grid(int device) {
+  const int key = 2 * D + (FP8 ? 1 : 0);
   {
     std::lock_guard<std::mutex> lock(g_occ_mutex);
     auto it = g_occ.find({device, key});
-    if (it != g_occ.end()) {
-      per_cu = it->second & 0xffff;
-      cus = it->second >> 16;
-    }
+    if (it != g_occ.end()) return it->second;
   }
-  if (per_cu == 0) {
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-      return -1;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, paged_decode_bf16_persistent_kernel<G, PB, FP8, DMA>, kDecodeThreads, 0) !=
-        hipSuccess)
-      return -1;
-    if (per_cu < 1) per_cu = 1;
-    std::lock_guard<std::mutex> lock(g_occ_mutex);
-    g_occ[{device, key}] = (cus << 16) | per_cu;
-  }
-  // bf16: two workgroups per CU (8 waves, 16 KB of K/V in flight each) measured
-  // faster than the register-limited maximum of three, whose extra streams of
-  // random 4 KB block-heads only add contention in the memory system.
-  constexpr int kCap = persistent_waves(G, FP8 && !DMA);
-  const int full = cus * (per_cu < kCap ? per_cu : kCap);
-  return upper < full ? upper : full;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_split_kernel<D, FP8>,
+                                                   kDecodeThreads, 0) != hipSuccess)
+    return -1;
+  per_cu = per_cu < 1 ? 1 : (per_cu > 2 ? 2 : per_cu);
+  int grid = cus * per_cu;
+  grid = grid < 1 ? 1 : (grid > kSplitMaxGrid ? kSplitMaxGrid : grid);
+  std::lock_guard<std::mutex> lock(g_occ_mutex);
+  g_occ[{device, key}] = grid;
+  return grid;
 }
 
-template <typename T, int D, int BS, int PB = kPartBlocks>
-void launch_combine(const DecodeParams& p, int batch, hipStream_t s) {
-  constexpr int kPairsPerGroup = kCombineThreads / kWave;
-  const int pairs = batch * p.num_heads;
-  hipLaunchKernelGGL((paged_decode_combine_kernel<T, D, BS, PB>),
-                     dim3((pairs + kPairsPerGroup - 1) / kPairsPerGroup), dim3(kCombineThreads), 0,
-                     s, p, batch);
-}
-
-// The persistent launch for query group G: longer partitions when the batch holds at
-// least kLongItemsPerWg items per workgroup; DMA selects the LDS-staged block loop.
-template <int G, bool FP8, bool DMA>
-int launch_persistent(const DecodeParams& p, const DecodeParams& pl, int batch, int device,
-                      int upper, int upper_long, int* counters, hipStream_t s, bool& long_items) {
-  const int grid_long = persistent_grid<G, FP8, kPartBlocksLong, DMA>(device, upper_long);
-  if (grid_long >= 1 && upper_long >= kLongItemsPerWg * grid_long) {
-    long_items = true;
-    hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<G, kPartBlocksLong, FP8, DMA>),
-                       dim3(grid_long), dim3(kDecodeThreads), 0, s, pl, batch, counters);
-    return NIA_OK;
-  }
-  const int grid = persistent_grid<G, FP8, kPartBlocks, DMA>(device, upper);
+template <int D, bool FP8>
+int launch_split(DecodeParams& p, int batch, hipStream_t s) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return NIA_ERR_LAUNCH;
+  const int grid = split_grid<D, FP8>(device);
   if (grid < 1) return NIA_ERR_LAUNCH;
-  hipLaunchKernelGGL((paged_decode_bf16_persistent_kernel<G, kPartBlocks, FP8, DMA>), dim3(grid),
-                     dim3(kDecodeThreads), 0, s, p, batch, counters);
-  return NIA_OK;
+  p.grid = grid;
+  if (batch > kSplitLdsBatch)
+    hipLaunchKernelGGL(decode_prefix_kernel, dim3(1), dim3(kDecodeThreads), 0, s, p, batch);
+  hipLaunchKernelGGL((decode_split_kernel<D, FP8>), dim3(grid), dim3(kDecodeThreads), 0, s, p,
+                     batch);
+  constexpr int kPairsPerGroup = kCombineThreads / kWave;
+  const int64_t pairs = (int64_t)batch * p.num_heads;
+  hipLaunchKernelGGL((decode_split_combine_kernel<D>),
+                     dim3((unsigned)((pairs + kPairsPerGroup - 1) / kPairsPerGroup)),
+                     dim3(kCombineThreads), 0, s, p, batch);
+  return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
-template <typename T, int D, int BS, bool FP8 = false>
-int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStream_t s) {
-  constexpr bool kBf16 = std::is_same<T, bf16_t>::value;
-  static_assert(kBf16 || !FP8, "fp8 caches take bf16 queries");
-  if (kBf16 && batch <= kPersistentMaxBatch) {
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) return NIA_ERR_LAUNCH;
-    const int upper = batch * p.num_kv_heads * (p.max_parts > 0 ? p.max_parts : 1);
-    // The longer partition: the (m, l) and o partials keep their places in the
-    // workspace, laid out for its smaller partition count.
-    DecodeParams pl = p;
-    pl.max_parts = decode_max_parts(p.max_blocks > 0 ? p.max_blocks : 1, kPartBlocksLong);
-    pl.ws_o = pl.ws_ml + (size_t)batch * p.num_heads * pl.max_parts * 2;
-    const int upper_long = batch * p.num_kv_heads * pl.max_parts;
-    // bf16 caches: block pairs staged through LDS, scores and P V on the matrix cores.
-    const bool dma = batch <= kDmaMaxBatch;
-    bool long_items = false;
-    int rc = NIA_OK;
-    switch (G) {
-#define NIA_CASE(GG)                                                                          \
-  case GG:                                                                                    \
-    if constexpr (staged_loop(GG, FP8)) {                                                     \
-      if (dma) {                                                                              \
-        rc = launch_persistent<GG, FP8, true>(p, pl, batch, device, upper, upper_long,        \
-                                              counters, s, long_items);                       \
-        break;                                                                                \
-      }                                                                                       \
-    }                                                                                         \
-    rc = launch_persistent<GG, FP8, false>(p, pl, batch, device, upper, upper_long, counters,  \
-                                           s, long_items);                                    \
-    break;
-      NIA_CASE(1)
-      NIA_CASE(2)
-      NIA_CASE(3)
-      NIA_CASE(4)
-      NIA_CASE(5)
-      NIA_CASE(6)
-      NIA_CASE(7)
-      NIA_CASE(8)
-#undef NIA_CASE
-      default:
-        return NIA_ERR_UNSUPPORTED;
-    }
-    if (rc != NIA_OK) return rc;
-    if (long_items) {
-      if (pl.max_parts > 1) launch_combine<T, D, BS, kPartBlocksLong>(pl, batch, s);
-    } else if (p.max_parts > 1) {
-      launch_combine<T, D, BS>(p, batch, s);
-    }
-    return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
-  }
+int launch_f32_partitions(const DecodeParams& p, int G, int batch, hipStream_t s) {
   const dim3 grid(p.max_parts, p.num_kv_heads, batch);
   switch (G) {
 #define NIA_CASE(GG)                                                                          \
   case GG:                                                                                    \
-    if constexpr (kBf16)                                                                      \
-      hipLaunchKernelGGL((paged_decode_bf16_kernel<GG, kPartBlocks, FP8>), grid,              \
-                         dim3(kDecodeThreads), 0, s, p);                                      \
-    else                                                                                      \
-      hipLaunchKernelGGL((paged_decode_partial_kernel<T, D, GG, BS, kPartBlocks>), grid,      \
-                         dim3(kDecodeThreads), 0, s, p);                                      \
+    hipLaunchKernelGGL((paged_decode_partial_kernel<float, 128, GG, 16, kPartBlocks>), grid,  \
+                       dim3(kDecodeThreads), 0, s, p);                                        \
     break;
     NIA_CASE(1)
     NIA_CASE(2)
@@ -1542,19 +1187,34 @@ int launch_decode(const DecodeParams& p, int G, int batch, int* counters, hipStr
     default:
       return NIA_ERR_UNSUPPORTED;
   }
-  if (p.max_parts > 1) launch_combine<T, D, BS>(p, batch, s);
+  if (p.max_parts > 1) {
+    constexpr int kPairsPerGroup = kCombineThreads / kWave;
+    const int pairs = batch * p.num_heads;
+    hipLaunchKernelGGL((paged_decode_combine_kernel<float, 128, 16, kPartBlocks>),
+                       dim3((pairs + kPairsPerGroup - 1) / kPairsPerGroup), dim3(kCombineThreads),
+                       0, s, p, batch);
+  }
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
 }  // namespace
 
 extern "C" size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_heads,
+                                                  int32_t num_kv_heads,
                                                   int32_t max_blocks_per_seq,
-                                                  int32_t block_size, int32_t head_dim) {
-  (void)block_size;
-  if (batch <= 0 || num_heads <= 0 || max_blocks_per_seq < 0 || head_dim <= 0) return 0;
-  const size_t parts = (size_t)decode_max_parts(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1);
-  return kCounterBytes + (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
+                                                  int32_t block_size, int32_t head_dim,
+                                                  int32_t dtype) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      max_blocks_per_seq < 0 || head_dim <= 0)
+    return 0;
+  const int32_t group = num_heads / num_kv_heads;
+  if (dtype == NIA_DTYPE_F32) {
+    if (!f32_partition_shape(head_dim, block_size, group)) return kHeaderBytes;
+    const size_t parts = (size_t)decode_max_parts(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1);
+    return kHeaderBytes +
+           (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
+  }
+  return split_workspace(batch, group, head_dim);
 }
 
 namespace {
@@ -1572,22 +1232,56 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
       bt_stride < max_blocks_per_seq || num_blocks < 0)
     return NIA_ERR_INVALID_ARGUMENT;
   if (num_heads % num_kv_heads != 0) return NIA_ERR_INVALID_ARGUMENT;
+  if (!(scale > 0.f) || scale == INFINITY) return NIA_ERR_INVALID_ARGUMENT;
   if (batch == 0) return NIA_OK;
   if (!out || !q || !context_lens || (max_blocks_per_seq > 0 && !block_tables))
     return NIA_ERR_INVALID_ARGUMENT;
   if (max_blocks_per_seq > 0 && (!k_cache || !v_cache)) return NIA_ERR_INVALID_ARGUMENT;
   if (fp8 && max_blocks_per_seq > 0 && (!k_scale || !v_scale)) return NIA_ERR_INVALID_ARGUMENT;
-  const int G = num_heads / num_kv_heads;
-  if (head_dim != 128 || block_size != 16 || G > 8) return NIA_ERR_UNSUPPORTED;
+  // the fp8 loop reads a tile's row scales before it knows the block is valid (block 0's
+  // rows stand in), so the pool must hold a block
+  if (fp8 && max_blocks_per_seq > 0 && num_blocks == 0) return NIA_ERR_INVALID_ARGUMENT;
   if (dtype != NIA_DTYPE_BF16 && (fp8 || dtype != NIA_DTYPE_F32)) return NIA_ERR_UNSUPPORTED;
-  const int64_t vec = dtype == NIA_DTYPE_BF16 ? 8 : 4;
-  if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
-      q_batch_stride % vec || q_head_stride % vec)
-    return NIA_ERR_MISALIGNED;
-  // the matrix-core loop reads a block-head's row scales four at a time (16 bytes)
-  if (fp8 && ((uintptr_t)k_scale % 16 || (uintptr_t)v_scale % 16)) return NIA_ERR_MISALIGNED;
+  const int G = num_heads / num_kv_heads;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NIA_DTYPE_BF16 && !split_shape(fp8, head_dim, block_size, G))
+    return NIA_ERR_UNSUPPORTED;
 
-  DecodeParams p;
+  if (dtype == NIA_DTYPE_F32 && !f32_partition_shape(head_dim, block_size, G)) {
+    // other fp32 shapes: the fp32 prefill kernel with one query row per sequence (any block
+    // size, head_dim 64 / 80 / 96 / 128, any group)
+    if (head_dim != 64 && head_dim != 80 && head_dim != 96 && head_dim != 128)
+      return NIA_ERR_UNSUPPORTED;
+    if (block_size <= 0) return NIA_ERR_UNSUPPORTED;
+    if ((uintptr_t)q % 16 || q_batch_stride % 4 || q_head_stride % 4 || (uintptr_t)out % 16 ||
+        out_batch_stride % 4 || out_head_stride % 4 || (uintptr_t)k_cache % 16 ||
+        (uintptr_t)v_cache % 16)
+      return NIA_ERR_MISALIGNED;
+    PrefillF32Params f{};
+    f.o = (float*)out;
+    f.o_tok = out_batch_stride;
+    f.o_head = out_head_stride;
+    f.q = (const float*)q;
+    f.q_tok = q_batch_stride;
+    f.q_head = q_head_stride;
+    f.k = (const float*)k_cache;
+    f.v = (const float*)v_cache;
+    f.ctx_len = context_lens;
+    f.block_tables = block_tables;
+    f.bt_stride = bt_stride;
+    f.max_blocks = max_blocks_per_seq;
+    f.num_blocks = num_blocks;
+    f.block_size = block_size;
+    f.num_heads = num_heads;
+    f.num_kv_heads = num_kv_heads;
+    f.group = G;
+    f.causal = NIA_CAUSAL_BOTTOM_RIGHT;
+    f.decode = 1;
+    f.scale_log2 = (double)scale * 1.4426950408889634;
+    return launch_prefill_f32(f, true, head_dim, batch, 1, s);
+  }
+
+  DecodeParams p{};
   p.out = out;
   p.out_b = out_batch_stride;
   p.out_h = out_head_stride;
@@ -1606,20 +1300,49 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
   p.num_kv_heads = num_kv_heads;
   p.num_blocks = num_blocks;
   p.scale_log2 = scale * kLog2e;
-  p.max_parts = decode_max_parts(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1);
-  const size_t need = nia_paged_decode_workspace_size(batch, num_heads, max_blocks_per_seq,
-                                                      block_size, head_dim);
+  p.group = G;
+  const size_t need = nia_paged_decode_workspace_size(batch, num_heads, num_kv_heads,
+                                                      max_blocks_per_seq, block_size, head_dim,
+                                                      dtype);
   if (!workspace || workspace_bytes < need) return NIA_ERR_WORKSPACE;
   if ((uintptr_t)workspace % 256) return NIA_ERR_MISALIGNED;
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  int* counters = reinterpret_cast<int*>(ws);
-  p.ws_ml = reinterpret_cast<float*>(ws + kCounterBytes);
-  p.ws_o = p.ws_ml + (size_t)batch * num_heads * p.max_parts * 2;
 
-  hipStream_t s = (hipStream_t)stream;
-  if (fp8) return launch_decode<bf16_t, 128, 16, true>(p, G, batch, counters, s);
-  if (dtype == NIA_DTYPE_BF16) return launch_decode<bf16_t, 128, 16>(p, G, batch, counters, s);
-  return launch_decode<float, 128, 16>(p, G, batch, counters, s);
+  if (dtype == NIA_DTYPE_F32) {
+    if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
+        q_batch_stride % 4 || q_head_stride % 4)
+      return NIA_ERR_MISALIGNED;
+    p.max_parts = decode_max_parts(max_blocks_per_seq > 0 ? max_blocks_per_seq : 1);
+    p.ws_ml = reinterpret_cast<float*>(ws + kHeaderBytes);
+    p.ws_o = p.ws_ml + (size_t)batch * num_heads * p.max_parts * 2;
+    return launch_f32_partitions(p, G, batch, s);
+  }
+
+  // bf16 queries over bf16 caches or the fp8 format: the split kernel
+  if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
+      q_batch_stride % 8 || q_head_stride % 8 || (uintptr_t)out % 8 || out_batch_stride % 4 ||
+      out_head_stride % 4)
+    return NIA_ERR_MISALIGNED;
+  // the fp8 loop reads a tile's row scales four at a time (16 bytes)
+  if (fp8 && ((uintptr_t)k_scale % 16 || (uintptr_t)v_scale % 16)) return NIA_ERR_MISALIGNED;
+  p.bs_log2 = __builtin_ctz((unsigned)block_size);
+  p.hg = num_kv_heads % 4 == 0 ? 4 : (num_kv_heads % 2 == 0 ? 2 : 1);
+  p.wph = 4 / p.hg;
+  p.nhg = num_kv_heads / p.hg;
+  p.ws_pfx = reinterpret_cast<int32_t*>(ws + kHeaderBytes);
+  p.sp_ml = reinterpret_cast<float*>(ws + kHeaderBytes + split_pfx_bytes(batch));
+  p.sp_o = p.sp_ml + split_rows(G) * 2;
+  if (fp8) return launch_split<128, true>(p, batch, s);
+  switch (head_dim) {
+    case 64:
+      return launch_split<64, false>(p, batch, s);
+    case 80:
+      return launch_split<80, false>(p, batch, s);
+    case 96:
+      return launch_split<96, false>(p, batch, s);
+    default:
+      return launch_split<128, false>(p, batch, s);
+  }
 }
 
 }  // namespace
@@ -1690,7 +1413,7 @@ void* device_scratch(int device, hipStream_t stream) {
   void* ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
   hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(64), 0, stream,
-                     reinterpret_cast<uint32_t*>(ptr), (int)(kCounterBytes / 4));
+                     reinterpret_cast<uint32_t*>(ptr), (int)(kHeaderBytes / 4));
   if (hipGetLastError() != hipSuccess) return nullptr;
   if (g_scratch_ptr.size() <= (size_t)device) g_scratch_ptr.resize(device + 1, nullptr);
   g_scratch_ptr[device] = ptr;
@@ -1712,8 +1435,10 @@ extern "C" int32_t nia_paged_decode_noalloc(void* out, int64_t out_batch_stride,
                                             void* stream) {
   if (batch < 0 || num_heads <= 0 || max_blocks_per_seq < 0) return NIA_ERR_INVALID_ARGUMENT;
   if (batch == 0) return NIA_OK;
-  const size_t need = nia_paged_decode_workspace_size(batch, num_heads, max_blocks_per_seq,
-                                                      block_size, head_dim);
+  if (num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return NIA_ERR_INVALID_ARGUMENT;
+  const size_t need = nia_paged_decode_workspace_size(batch, num_heads, num_kv_heads,
+                                                      max_blocks_per_seq, block_size, head_dim,
+                                                      dtype);
   if (need > kScratchBytes) return NIA_ERR_SCRATCH_LIMIT;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0) return NIA_ERR_LAUNCH;

@@ -28,6 +28,7 @@ struct PrefillF32Params {
   int32_t num_kv_heads;
   int32_t group;
   int32_t causal;
+  int32_t decode;  // one query row per sequence: row s of q / o (q_start, q_len unused)
   double scale_log2;
 };
 

@@ -49,7 +49,8 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
   const int mb = blockIdx.x;
   const int h = blockIdx.y;
   const int seq = blockIdx.z;
-  const int qlen = p.q_len[seq];
+  const int qlen = p.decode ? 1 : p.q_len[seq];
+  const int64_t qstart = p.decode ? seq : p.q_start[seq];
   const int m0 = mb * kF32BlockM;
   if (qlen <= 0 || m0 >= qlen) return;  // uniform over the workgroup
   int klen;
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
   // B operand of S^T: q[r][16 c + 4 slot + i] widened to fp64
   double qd[D / 4];
   {
-    const float* qp = p.q + (p.q_start[seq] + (int64_t)(row_ok ? r : 0)) * p.q_tok +
+    const float* qp = p.q + (qstart + (int64_t)(row_ok ? r : 0)) * p.q_tok +
                       (int64_t)h * p.q_head;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
   l_run += __shfl_xor(l_run, 32, kWave);
   if (!row_ok) return;
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  float* op = p.o + (p.q_start[seq] + (int64_t)r) * p.o_tok + (int64_t)h * p.o_head;
+  float* op = p.o + (qstart + (int64_t)r) * p.o_tok + (int64_t)h * p.o_head;
 #pragma unroll
   for (int t = 0; t < D / 16; ++t)
     *reinterpret_cast<float4*>(op + 16 * t + 4 * slot) =

@@ -146,29 +146,69 @@ def kv_write(
 # ---------------------------------------------------------------------------------
 
 
-def decode_workspace_bytes(batch: int, num_heads: int, max_blocks: int, block_size: int,
-                           head_dim: int) -> int:
+def decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, max_blocks: int,
+                           block_size: int, head_dim: int, dtype=torch.bfloat16) -> int:
+    """Bytes of decode workspace a call with these sizes needs (``dtype``: the query
+    dtype; fp8 caches take bf16 queries)."""
     return int(
-        _lib.load().nia_paged_decode_workspace_size(batch, num_heads, max_blocks, block_size,
-                                                    head_dim)
-    )
+        _lib.load().nia_paged_decode_workspace_size(batch, num_heads, num_kv_heads, max_blocks,
+                                                    block_size, head_dim,
+                                                    _dtype_code_of(dtype)))
 
 
+def _dtype_code_of(dtype) -> int:
+    if dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return _DTYPES[dtype]
+
+
+def check_decode_shape(head_dim: int, block_size: int, num_heads: int, num_kv_heads: int,
+                       dtype=torch.bfloat16, fp8_cache: bool = False) -> None:
+    """Raise ValueError unless paged decode supports this layout (the limits of
+    include/nia_attn.h): bf16 - block size a power of two >= 4, head_dim 64 / 80 / 96 /
+    128, at most 16 query heads per KV head; fp8 caches - head_dim 128, block size a
+    power of two >= 16; fp32 - head_dim 64 / 80 / 96 / 128, any block size and group.
+    A KV pool can be checked when it is built, before any step runs."""
+    if num_kv_heads <= 0 or num_heads % num_kv_heads != 0:
+        raise ValueError(f"num_heads must be divisible by num_kv_heads, got {num_heads=} and "
+                         f"{num_kv_heads=}")
+    if head_dim not in (64, 80, 96, 128):
+        raise ValueError(f"paged decode supports head_dim 64, 80, 96 or 128, not {head_dim}")
+    if block_size <= 0:
+        raise ValueError(f"block_size must be positive, got {block_size}")
+    if dtype == torch.float32 and not fp8_cache:
+        return
+    pow2 = block_size & (block_size - 1) == 0
+    if fp8_cache:
+        if head_dim != 128 or not pow2 or block_size < 16:
+            raise ValueError("fp8 KV caches need head_dim 128 and a power-of-two block size "
+                             f">= 16 (got head_dim {head_dim}, block_size {block_size})")
+    elif not pow2 or block_size < 4:
+        raise ValueError("bf16 paged decode needs a power-of-two block size >= 4, "
+                         f"got {block_size}")
+    if num_heads // num_kv_heads > 16:
+        raise ValueError("bf16 paged decode takes at most 16 query heads per KV head, got "
+                         f"{num_heads // num_kv_heads}")
+
+
+# One workspace per (device, stream): calls on one stream run one after another and may
+# share it; calls on other streams get their own.  A workspace that is outgrown is kept
+# (in _RETIRED) rather than freed, since a captured HIP graph may still hold its address.
 _DECODE_WS: dict = {}
+_RETIRED: list = []
 
 
-def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A zero-initialised decode workspace of at least ``nbytes``, cached per device.
-
-    The decode kernel keeps its work counters at the start of the workspace and
-    returns them to zero at the end of every call, so a workspace must be zero
-    once, before its first use, and then serves any number of calls made one
-    after another on one stream.
-    """
-    key = torch.device(device)
+def decode_workspace(device: torch.device, nbytes: int, stream=None) -> torch.Tensor:
+    """A decode workspace of at least ``nbytes`` for (``device``, ``stream``) (default: the
+    device's current stream), cached and reused by later calls on that stream."""
+    dev = torch.device(device)
+    st = torch.cuda.current_stream(dev) if stream is None else stream
+    key = (dev, st.cuda_stream)
     ws = _DECODE_WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=key)
+        if ws is not None:
+            _RETIRED.append(ws)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _DECODE_WS[key] = ws
     return ws
 
@@ -191,8 +231,8 @@ def paged_decode(
     for S_step = 1.  q: (B, H, D) or (B, 1, H, D); k_cache/v_cache: one layer,
     [num_blocks, H_kv, BS, D]; block_tables: (B, max_blocks) int32;
     context_lens: (B,) int64.  Returns (B, H, D) (or q's 4-D shape).
-    ``workspace`` (optional, uint8) must have been zero before its first use
-    (see ``decode_workspace``); by default a cached per-device one is used.
+    ``workspace`` (optional, uint8, at least ``decode_workspace_bytes(...)``); by
+    default the cached one of the current stream (``decode_workspace``) is used.
     fp8 caches (uint8 / float8_e4m3fn codes) take their per-row ``k_scale`` /
     ``v_scale`` [num_blocks, H_kv, BS] float32 and bf16 queries.
     """
@@ -240,7 +280,8 @@ def paged_decode(
             raise ValueError("out must match q's shape and dtype")
         _last_contig("out", out3)
     max_blocks = block_tables.shape[1]
-    need = decode_workspace_bytes(b, h, max_blocks, bs, d)
+    check_decode_shape(d, bs, h, hkv, q3.dtype, fp8)
+    need = decode_workspace_bytes(b, h, hkv, max_blocks, bs, d, q3.dtype)
     if workspace is None:
         workspace = decode_workspace(dev, need)
     ws_bytes = workspace.numel() * workspace.element_size()

@@ -52,9 +52,13 @@ def test_validation_returns_codes_without_launching():
     # decode: heads not divisible
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 6, 4, 128, 16, 10, 0.1,
                                 None, 0, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    # decode: unsupported head_dim
+    # decode: unsupported head_dim; bf16 block size 2; a group of 32
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 72, 16, 10, 0.1,
                                 None, 0, 0, None) == _lib.ERR_UNSUPPORTED
+    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 128, 2, 10, 0.1,
+                                p, 1 << 30, 0, None) == _lib.ERR_UNSUPPORTED
+    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 32, 1, 128, 16, 10, 0.1,
+                                p, 1 << 30, 0, None) == _lib.ERR_UNSUPPORTED
     # decode: workspace too small for 2 partitions
     assert lib.nia_paged_decode(p, 128, 128, p, 1024, 128, p, p, p, 64, 64, p, 2, 8, 4, 128, 16,
                                 100, 0.1, None, 0, 0, None) == _lib.ERR_WORKSPACE
@@ -76,11 +80,11 @@ def test_validation_returns_codes_without_launching():
 def test_noalloc_decode_refuses_sizes_beyond_its_scratch_without_launching():
     lib = _lib.load()
     p = ctypes.c_void_p(16)  # never dereferenced: the size check comes first
-    # 4096 sequences x 64 heads x 256 partitions of partials: far beyond the fixed array
-    need = lib.nia_paged_decode_workspace_size(4096, 64, 8192, 16, 128)
+    # fp32 partitions: 4096 sequences x 64 heads x 256 partitions, far beyond the array
+    need = lib.nia_paged_decode_workspace_size(4096, 64, 8, 8192, 16, 128, 1)
     assert need > _lib.DECODE_SCRATCH_BYTES
     assert lib.nia_paged_decode_noalloc(p, 0, 0, p, 0, 0, p, p, p, 8192, 8192, p, 4096, 64, 8,
-                                        128, 16, 10, 0.1, 0, None) == _lib.ERR_SCRATCH_LIMIT
+                                        128, 16, 10, 0.1, 1, None) == _lib.ERR_SCRATCH_LIMIT
     assert lib.nia_paged_decode_noalloc(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 0, 8, 4, 128, 16,
                                         10, 0.1, 0, None) == _lib.OK  # empty batch
     assert lib.nia_paged_decode_noalloc(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, -1, 8, 4, 128, 16,
@@ -89,12 +93,22 @@ def test_noalloc_decode_refuses_sizes_beyond_its_scratch_without_launching():
 
 def test_workspace_size():
     lib = _lib.load()
-    # 256 B of work counters, then (m, l) and the partial output per
-    # (sequence, head, partition).
-    counters = 256
-    assert lib.nia_paged_decode_workspace_size(64, 32, 32, 16, 128) == counters + 64 * 32 * 130 * 4
-    assert lib.nia_paged_decode_workspace_size(64, 32, 512, 16, 128) == \
-        counters + 64 * 32 * 16 * 130 * 4
+    hdr = 256
+    # bf16 (and fp8): the unit prefix (batch + 1 ints, rounded to 256 B), then (m, l) and
+    # the partial output of 8 G rows per workgroup for a grid of at most 512
+    pfx = -(-(64 + 1) * 4 // 256) * 256
+    assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, 16, 128, 0) == \
+        hdr + pfx + 512 * 8 * 4 * 130 * 4
+    assert lib.nia_paged_decode_workspace_size(64, 32, 8, 32, 16, 80, 0) == \
+        hdr + pfx + 512 * 8 * 4 * 82 * 4
+    # fp32 at head_dim 128 / block 16: partitions of 32 blocks per (sequence, head)
+    assert lib.nia_paged_decode_workspace_size(64, 32, 8, 32, 16, 128, 1) == \
+        hdr + 64 * 32 * 130 * 4
+    assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, 16, 128, 1) == \
+        hdr + 64 * 32 * 16 * 130 * 4
+    # fp32 other shapes run without partials
+    assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, 32, 128, 1) == hdr
+    assert lib.nia_paged_decode_workspace_size(64, 32, 3, 512, 16, 128, 0) == 0  # 32 % 3
 
 
 def test_qk_norm_rope_validation_without_launching():

@@ -80,25 +80,26 @@ def test_decode_block_boundaries(group, dtype):
     assert_attn_close(out, oracle_decode(c), dtype, f"boundaries G={group}")
 
 
-def test_long_partitions_at_their_boundaries():
-    """A batch wide enough (40 sequences x 8 KV heads, 512-block tables) that the
-    persistent kernel takes 48-block partitions (768 tokens): contexts on both sides of
-    one, two and three of them, a single token, a full table, and a sequence whose
-    context is cut to zero after the write."""
+def test_long_contexts_and_a_zeroed_context():
+    """A Qwen3-8B-wide batch (40 sequences x 8 KV heads, 512-block tables): contexts on
+    both sides of 768-token multiples, a single token, a full table; then one context
+    cut to zero after the write (its output is zeros; the others still match the oracle,
+    though not bit for bit: the key ranges of the waves move with the total)."""
     lens = [1, 16, 17, 767, 768, 769, 1535, 1536, 1537, 2303, 2304, 2305, 8192, 8191, 4000]
     lens += [int(x) for x in torch.randint(1, 8193, (40 - len(lens),),
                                            generator=torch.Generator().manual_seed(48))]
     c = workloads.make_decode(len(lens), 32, 8, 128, lens, 40000, 16, torch.bfloat16, "cuda",
                               seed=480, max_blocks=512)
     out = run_step(c)
-    assert_attn_close(out, oracle_decode(c), torch.bfloat16, "long partitions")
+    exp = oracle_decode(c)
+    assert_attn_close(out, exp, torch.bfloat16, "long contexts")
     ctx = c.context_lens.clone()
     ctx[5] = 0
     out0 = ops.paged_decode(c.q, c.k_cache[0], c.v_cache[0], c.block_tables, ctx)
     torch.cuda.synchronize()
     assert out0[5].eq(0).all()
     keep = [i for i in range(len(lens)) if i != 5]
-    assert torch.equal(out0[keep], out[keep])
+    assert_attn_close(out0[keep], exp[keep], torch.bfloat16, "long contexts, one zeroed")
 
 
 @pytest.mark.parametrize("batch", [1024, 1025])
