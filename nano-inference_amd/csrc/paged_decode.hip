@@ -520,7 +520,8 @@ NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
 
 constexpr int kSlotBytes = 16384;      // a wave's LDS slot: [K tile 0][V tile 0][K tile 1][V tile 1]
 constexpr int kUnitKeys = 32;          // keys per unit (two 16-key tiles)
-constexpr int kSplitLdsBatch = 2048;   // batches whose unit prefix each workgroup builds in LDS
+constexpr int kSplitLdsBatch = 1024;   // batches whose unit prefix (and context lengths) each
+                                       // workgroup builds in LDS
 constexpr int kSplitMaxGrid = 512;     // workgroups at most (sizes the partial slots)
 
 // 16-byte DMA global -> LDS with a wave-uniform byte offset (soffset) on top of the lane's.
@@ -588,10 +589,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   constexpr int kDt = D / 16;             // PV tiles of 16 dims
   __shared__ __attribute__((aligned(1024))) uint8_t s_dma[kDecodeWaves * kSlotBytes];
   __shared__ int s_pfx[kSplitLdsBatch + 1];
+  __shared__ int s_ctx[kSplitLdsBatch];
   __shared__ int s_wave[kDecodeWaves];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  // wave-uniform, and said so: everything derived from it (the unit walk, block ids, buffer
+  // resources, LDS bases) then stays in scalar registers, without waterfall loops
+  const int wave = uniform(tid / kWave);
   const int hn = lane & 15;    // query head of the group in this lane's accumulator column
   const int quad = lane >> 4;  // rows (keys / dims) 4 quad .. + 3 of the accumulators
   const int bs_log2 = p.bs_log2;
@@ -599,9 +603,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   const int64_t cap = (int64_t)p.max_blocks << bs_log2;
   const int G = p.group;
 
-  // ---- units before each sequence (one head group) ----------------------------------------
+  // ---- units before each sequence (one head group), and the clamped context lengths -------
   const int* pfx = p.ws_pfx;  // large batches: written by decode_prefix_kernel
-  if (batch <= kSplitLdsBatch) {
+  const bool lds_index = batch <= kSplitLdsBatch;
+  if (lds_index) {
     constexpr int kPer = kSplitLdsBatch / kDecodeThreads;
     const int b0 = tid * kPer;
     int units[kPer];
@@ -610,6 +615,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     for (int k = 0; k < kPer; ++k) {
       int64_t c = b0 + k < batch ? p.context_lens[b0 + k] : 0;
       c = c < 0 ? 0 : (c > cap ? cap : c);
+      if (b0 + k < batch) s_ctx[b0 + k] = (int)c;
       units[k] = (int)((c + kUnitKeys - 1) / kUnitKeys);
       run += units[k];
     }
@@ -652,9 +658,14 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     x.j = r - p0;
     x.n = uniform(pfx[x.b + 1]) - p0;
     x.U0 = (int64_t)x.g * T + p0;
-    int64_t c = p.context_lens[x.b];
-    c = c < 0 ? 0 : (c > cap ? cap : c);
-    x.ctx = uniform((int)c);
+    int c;
+    if (lds_index) {
+      c = s_ctx[x.b];
+    } else {
+      const int64_t c64 = p.context_lens[x.b];
+      c = (int)(c64 < 0 ? 0 : (c64 > cap ? cap : c64));
+    }
+    x.ctx = uniform(c);
   };
   auto advance = [&](SplitUnit& x) __attribute__((always_inline)) {
     if (x.u < 0) return;
@@ -669,19 +680,21 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
       locate(x.u + 1, x);
     }
   };
-  // Lanes 0 .. 7: the blocks of a unit's 32 keys, (32 j >> bs_log2) + lane; -1 past the
-  // context, past the unit or for an id outside [0, num_blocks).
+  // Lanes 0 .. 7: the table entries of a unit's 32 keys, blocks (32 j >> bs_log2) + lane;
+  // -1 past the context or past the unit.  The entries are checked against [0, num_blocks)
+  // where they are used: a check here would wait for the load (and with it for every load
+  // in flight, the DMA of the next unit included).
   auto load_ids = [&](const SplitUnit& x) __attribute__((always_inline)) -> int {
     if (x.u < 0) return -1;
     const int k0 = kUnitKeys * x.j;
     const int bi = (k0 >> bs_log2) + lane;
     const int last = (min(k0 + kUnitKeys, x.ctx) - 1) >> bs_log2;
     int id = -1;
-    if (lane < 8 && bi <= last) {
-      id = p.block_tables[(int64_t)x.b * p.bt_stride + bi];
-      if (id < 0 || (int64_t)id >= p.num_blocks) id = -1;
-    }
+    if (lane < 8 && bi <= last) id = p.block_tables[(int64_t)x.b * p.bt_stride + bi];
     return id;
+  };
+  auto valid_block = [&](int blk) __attribute__((always_inline)) -> int {
+    return (blk < 0 || (int64_t)blk >= p.num_blocks) ? -1 : blk;
   };
 
   const SplitLane<D> off = split_lane<D>(lane);
@@ -691,7 +704,11 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   // DMA of unit x's two tiles (KV head hk) into the slot.  Groups of 4 rows past the
   // context or in an invalid block issue nothing; their keys are masked after the read.
   auto issue = [&](const SplitUnit& x, int ids, int hk) __attribute__((always_inline)) {
-    const int k0 = kUnitKeys * x.j;
+    // the unit's fields are wave-uniform; saying so keeps the buffer resources and offsets
+    // in scalar registers (the compiler cannot see through the unit walk's loops)
+    hk = uniform(hk);
+    const int k0 = uniform(kUnitKeys * x.j);
+    const int ctx = uniform(x.ctx);
     const int bi0 = k0 >> bs_log2;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -699,16 +716,15 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
       if constexpr (FP8) {
         // a tile lies in one block (block size >= 16)
         const int key = k0 + 16 * t;
-        const int blk = key < x.ctx ? __builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0) : -1;
-        // the scales are read for every tile (block 0's rows stand in for a missing block)
-        // and zeroed after the read
+        const int blk =
+            key < ctx ? valid_block(__builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0)) : -1;
+        // the scales are read for every tile (block 0's rows stand in for a missing block or
+        // a tile past the context): the keys they belong to are masked where they are used,
+        // and nothing here may consume the loads (that would wait for the DMA in flight)
         const int64_t head = ((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << bs_log2;
         const int64_t row0 = head + (key & bs_mask) + 4 * quad;
-        const float4 kq = *reinterpret_cast<const float4*>(p.k_scale + row0);
-        const float4 vq = *reinterpret_cast<const float4*>(p.v_scale + row0);
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        ks[t] = blk >= 0 ? kq : z;
-        vs[t] = blk >= 0 ? vq : z;
+        ks[t] = *reinterpret_cast<const float4*>(p.k_scale + row0);
+        vs[t] = *reinterpret_cast<const float4*>(p.v_scale + row0);
         if (blk >= 0) {
           const uint8_t* kb = reinterpret_cast<const uint8_t*>(p.k_cache) + head * 128;
           const uint8_t* vb = reinterpret_cast<const uint8_t*>(p.v_cache) + head * 128;
@@ -731,7 +747,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int key = k0 + 16 * t + 4 * j;  // rows 4 j .. + 3 lie in one block (>= 4 rows)
-          const int blk = key < x.ctx ? __builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0) : -1;
+          const int blk =
+              key < ctx ? valid_block(__builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0)) : -1;
           if (blk >= 0) {
             const int64_t head = ((int64_t)blk * p.num_kv_heads + hk) << bs_log2;
             const int bytes = (D * 2) << bs_log2;
@@ -812,8 +829,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   advance(n2);
   int ids_c = load_ids(cur);
   int ids_1 = load_ids(n1);
-  uint4 qb[4], qn[4];
-  uint2 qt = make_uint2(0, 0), qnt = make_uint2(0, 0);
+  uint4 qb[4];
+  uint2 qt = make_uint2(0, 0);
   load_q(cur, qb, qt);
   issue(cur, ids_c, cur.g * hg + hig);
   for (;;) {
@@ -861,17 +878,15 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     __builtin_amdgcn_s_waitcnt(0);  // read out before the slot is refilled
     __builtin_amdgcn_sched_barrier(0);
     const bool new_seg = n1.u < 0 || n1.U0 != cur.U0;
-    if (n1.u >= 0) {
-      if (new_seg) load_q(n1, qn, qnt);
-      issue(n1, ids_1, n1.g * hg + hig);
-    }
+    if (n1.u >= 0) issue(n1, ids_1, n1.g * hg + hig);
     const int ids_2 = load_ids(n2);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- scores, masked past the context and in invalid blocks ------------------------------
     const int k0 = kUnitKeys * cur.j;
     const int bi0 = k0 >> bs_log2;
-    const uint32_t okmask = (uint32_t)__builtin_amdgcn_ballot_w64(ids_c >= 0) & 0xffu;
+    const uint32_t okmask =
+        (uint32_t)__builtin_amdgcn_ballot_w64(valid_block(ids_c) >= 0) & 0xffu;
     bool blk_ok[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -889,6 +904,9 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
         sc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
             kta[t], __builtin_bit_cast(s16x4_t, qt), sc[t], 0, 0, 0);
     }
+    // the next sequence's Q goes straight into the B operand registers, which this unit no
+    // longer needs (its first use follows the next wait for the slot)
+    if (new_seg && n1.u >= 0) load_q(n1, qb, qt);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if constexpr (FP8) {
@@ -964,9 +982,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
       l_run = 0.f;
 #pragma unroll
       for (int mt = 0; mt < kDt; ++mt) oacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qb[s] = qn[s];
-      qt = qnt;
     }
     if (n1.u < 0) break;
     cur = n1;
@@ -997,14 +1012,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_prefix_kernel(DecodePar
 }
 
 // Merge the partials of every (sequence, head) whose units were split over several waves'
-// ranges: one wave per pair.  Lane i takes the (m, l) of partial i (64 at a time), the
-// wave reduces the max and the weights, and each lane accumulates output dims lane,
-// lane + 64 over the partial rows, four rows per round of loads.  Pairs of empty
-// sequences get zeros; pairs finished by the split kernel are left alone.
+// ranges: one wave per pair, lane l owning output dims 2 l, 2 l + 1.  The partial rows of
+// up to kCombineRows ranges are loaded in one round (their (m, l) and the lane's two
+// dims), then merged online (running max, rescaled sums), so a pair costs two rounds of
+// loads after the unit prefix unless its sequence spans more ranges than that.  Pairs of
+// empty sequences get zeros; pairs finished by the split kernel are left alone.
+constexpr int kCombineRows = 16;
+
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(DecodeParams p,
                                                                                int batch) {
-  constexpr int DL = (D + kWave - 1) / kWave;
+  static_assert(D <= 2 * kWave, "two output dims per lane");
   const int lane = threadIdx.x & (kWave - 1);
   const int pair = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6);
   if (pair >= batch * p.num_heads) return;
@@ -1016,9 +1034,11 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
   const int T = p.ws_pfx[batch];
   const int pb = p.ws_pfx[b];
   const int n_units = p.ws_pfx[b + 1] - pb;
+  const int d0 = 2 * lane;
+  const bool has_dims = d0 < D;
   bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h;
   if (n_units <= 0) {
-    for (int d = lane; d < D; d += kWave) out[d] = (bf16_t)0.f;
+    if (has_dims) *reinterpret_cast<uint32_t*>(out + d0) = 0u;
     return;
   }
   const int64_t total = (int64_t)T * p.nhg;
@@ -1028,62 +1048,56 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
   const int64_t f = ((U0 + 1) * nv - 1) / total, e = (U1 * nv - 1) / total;
   if (f == e) return;  // one wave had the whole sequence and wrote it
   const int n = (int)(e - f + 1);
-  auto row_of = [&](int i, bool& live) -> int64_t {
-    const int64_t v = f + i;
-    const int64_t s0 = total * v / nv, s1 = total * (v + 1) / nv;
-    live = s0 < s1;  // an empty range wrote nothing
-    const int sl = U0 <= s0 ? 0 : 1;
-    return ((v * 2 + sl) * p.hg + hig) * G + gq;
-  };
-  float mt = -INFINITY;
-  for (int c0 = 0; c0 < n; c0 += kWave) {
-    bool live = false;
-    const int64_t row = c0 + lane < n ? row_of(c0 + lane, live) : 0;
-    if (live) mt = fmaxf(mt, p.sp_ml[2 * row]);
-  }
-  mt = wave_max(mt);
-  float ls = 0.f;
-  float acc[DL];
+  // range starts s(v) = floor(total * v / nv), stepped without divisions:
+  // s(v + 1) = s(v) + q + (carry of r over nv)
+  const int64_t q = total / nv, r = total - q * nv;
+  int64_t s_next = total * f / nv;
+  int64_t rem = total * f - s_next * nv;  // (total * v) mod nv
+  float m_run = -INFINITY, l_run = 0.f;
+  float2 acc = make_float2(0.f, 0.f);
+  for (int c0 = 0; c0 < n; c0 += kCombineRows) {
+    float2 ml[kCombineRows], o[kCombineRows];
 #pragma unroll
-  for (int k = 0; k < DL; ++k) acc[k] = 0.f;
-  for (int c0 = 0; c0 < n; c0 += kWave) {
-    bool live = false;
-    const int64_t row = c0 + lane < n ? row_of(c0 + lane, live) : 0;
-    float w = 0.f;
-    if (live) {
-      const float2 ml = *reinterpret_cast<const float2*>(p.sp_ml + 2 * row);
-      w = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - mt);
-      ls = fmaf(ml.y, w, ls);
-    }
-    const int cnt = min(kWave, n - c0);
-    for (int j0 = 0; j0 < cnt; j0 += 4) {
-      float r[4][DL];
-      float wj[4];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int src = (j0 + jj) & (kWave - 1);
-        wj[jj] = j0 + jj < cnt ? __shfl(w, src, kWave) : 0.f;
-        const int64_t rj = __shfl(row, src, kWave);
-#pragma unroll
-        for (int k = 0; k < DL; ++k) {
-          const int d = lane + kWave * k;
-          // rows of ranges that saw no key hold no data: weight 0 and not read
-          r[jj][k] = (wj[jj] > 0.f && d < D) ? p.sp_o[rj * D + d] : 0.f;
+    for (int i = 0; i < kCombineRows; ++i) {
+      ml[i] = make_float2(-INFINITY, 0.f);
+      o[i] = make_float2(0.f, 0.f);
+      const int64_t v = f + c0 + i;
+      if (c0 + i < n) {
+        const int64_t s0 = s_next;
+        rem += r;
+        s_next += q + (rem >= nv ? 1 : 0);
+        rem -= rem >= nv ? nv : 0;
+        const int64_t s1 = s_next;
+        if (s0 < s1) {  // an empty range wrote nothing
+          const int sl = U0 <= s0 ? 0 : 1;
+          const int64_t row = ((v * 2 + sl) * p.hg + hig) * G + gq;
+          ml[i] = *reinterpret_cast<const float2*>(p.sp_ml + 2 * row);
+          if (has_dims) o[i] = *reinterpret_cast<const float2*>(p.sp_o + row * D + d0);
         }
       }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int k = 0; k < DL; ++k) acc[k] = fmaf(r[jj][k], wj[jj], acc[k]);
     }
-  }
-  ls = wave_sum(ls);
-  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    float cm = m_run;
 #pragma unroll
-  for (int k = 0; k < DL; ++k) {
-    const int d = lane + kWave * k;
-    if (d < D) out[d] = (bf16_t)(acc[k] * inv);
+    for (int i = 0; i < kCombineRows; ++i) cm = fmaxf(cm, ml[i].x);
+    if (cm == -INFINITY) continue;  // no keys so far
+    const float corr = m_run == -INFINITY ? 0.f : fast_exp2(m_run - cm);
+    l_run *= corr;
+    acc.x *= corr;
+    acc.y *= corr;
+#pragma unroll
+    for (int i = 0; i < kCombineRows; ++i) {
+      // a range that saw no key has m = -inf and weight 0; its o is not read into the sum
+      const float w = ml[i].x == -INFINITY ? 0.f : fast_exp2(ml[i].x - cm);
+      l_run = fmaf(ml[i].y, w, l_run);
+      if (w > 0.f) {
+        acc.x = fmaf(o[i].x, w, acc.x);
+        acc.y = fmaf(o[i].y, w, acc.y);
+      }
+    }
+    m_run = cm;
   }
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  if (has_dims) *reinterpret_cast<uint32_t*>(out + d0) = pack_bf16x2(acc.x * inv, acc.y * inv);
 }
 
 constexpr int kPartBlocks = 32;  // fp32 partition kernel: 512 tokens per partition
