@@ -296,6 +296,22 @@ def bench_e2e(torch, mixed: bool, fp8_cache: bool = False):
                 kv_cache="fp8 (e4m3 + row scales)" if fp8_cache else "bf16")
 
 
+def bench_e2e_eager(torch):
+    """The Qwen3-0.6B generation of bench_e2e (prefill first) with every decode step run
+    eagerly, layer by layer, as the reference engine runs it (no HIP graph), and the host
+    time of every attention-path call: what the wrappers cost the CPU per call."""
+    from nano_inference_amd import e2e
+
+    gen = e2e.build(use_graph=False, mixed=False)
+    gen.run([pr[:64] for pr in gen.prompts[:4]])  # warm-up
+    with e2e.HostTimer() as ht:
+        st = gen.run(gen.prompts)
+    return dict(tokens_per_s=round(st.tokens_per_s, 1),
+                decode_tokens_per_s=round(st.decode_tokens_per_s, 1),
+                total_s=round(st.total_s, 4), scheduling="prefill first, eager decode steps",
+                host_per_call=ht.per_call_us())
+
+
 def cpu_baseline(torch, workloads, budget_s: float = 20.0):
     """The reference's decode attention (op-for-op CPU restatement), fp32, on a sample.
 
@@ -409,6 +425,7 @@ def main() -> int:
         extra["e2e_qwen3_0p6b"] = bench_e2e(torch, mixed=True)
         extra["e2e_qwen3_0p6b_prefill_first"] = bench_e2e(torch, mixed=False)
         extra["e2e_qwen3_0p6b_fp8_cache"] = bench_e2e(torch, mixed=True, fp8_cache=True)
+        extra["e2e_qwen3_0p6b_eager"] = bench_e2e_eager(torch)
     line = {
         "metric": "decode attn HBM GB/s (% of peak) + prefill attn TFLOP/s (% bf16 MFMA peak)",
         "value": round(value, 1),

@@ -36,12 +36,24 @@ from .context import AttentionMetadata, PackedAttentionMetadata
 from .layers import MRotaryEmbedding, RMSNorm, RotaryEmbedding
 
 
-def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int) -> torch.Tensor:
-    """Visible-key counts of a prefix mask; raises for any other mask shape.
+_PREFIX = ops.TensorMemo()
+
+
+def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int,
+                    device: torch.device) -> torch.Tensor:
+    """Visible-key counts (int32, on ``device``) of a prefix mask; raises for any other
+    mask shape.
 
     Accepts the reference's two mask forms: 2-D bool (B, S_total) with True =
     visible, or additive (B, 1, 1, S_total) with 0 = visible and -inf = masked.
+    Checking that the mask is a prefix reads it back to the host; the result is kept
+    per mask tensor (ops.TensorMemo), so the layers of a step that share one mask pay
+    for that once.  A mask on the CPU is checked there.
     """
+    key = (batch, key_len, device)
+    lens = _PREFIX.get(mask, key)
+    if lens is not None:
+        return lens
     if mask.dim() == 2:
         vis = mask[:, :key_len].to(torch.bool)
     elif mask.dim() == 4 and mask.shape[1] == 1 and mask.shape[2] == 1:
@@ -50,11 +62,13 @@ def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int) -> torch.Tenso
         raise NotImplementedError(f"attention_mask of shape {tuple(mask.shape)}")
     if vis.shape[0] != batch:
         vis = vis.expand(batch, -1)
-    lens = vis.sum(dim=-1)
+    n = vis.sum(dim=-1)
     ar = torch.arange(vis.shape[-1], device=vis.device)
-    if not torch.equal(vis, ar.unsqueeze(0) < lens.unsqueeze(1)):
+    if not torch.equal(vis, ar.unsqueeze(0) < n.unsqueeze(1)):
         raise NotImplementedError("only prefix (right-padding) attention masks are supported")
-    return lens.to(torch.int32)
+    lens = n.to(device=device, dtype=torch.int32)
+    _PREFIX.put(mask, key, lens)
+    return lens
 
 
 def scaled_dot_product_attention(
@@ -84,7 +98,7 @@ def scaled_dot_product_attention(
     ar = torch.arange(b, device=dev, dtype=torch.int32)
     q_len = torch.full((b,), sq, device=dev, dtype=torch.int32)
     if attention_mask is not None:
-        k_len = _prefix_lengths(attention_mask.to(dev), b, sk)
+        k_len = _prefix_lengths(attention_mask, b, sk, dev)
     else:
         k_len = torch.full((b,), sk, device=dev, dtype=torch.int32)
     out = ops.prefill(q3, k3, v3, ar * sq, q_len, ar * sk, k_len, sq, causal)
@@ -190,7 +204,7 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         dev = q.device
         ar = torch.arange(b, device=dev, dtype=torch.int32) * s
         lens = torch.full((b,), s, device=dev, dtype=torch.int32)
-        k_len = lens if attention_mask is None else _prefix_lengths(attention_mask.to(dev), b, s)
+        k_len = lens if attention_mask is None else _prefix_lengths(attention_mask, b, s, dev)
         return ops.prefill(
             q.reshape(b * s, self.num_heads, self.head_dim),
             k.reshape(b * s, self.num_kv_heads, self.head_dim),

@@ -666,6 +666,45 @@ class AttentionTimer:
                 "attention_share": attn / steps if steps > 0 else 0.0}
 
 
+class HostTimer:
+    """Context manager: host time (perf_counter) of every call made through the ``ops``
+    wrappers while active.  That is what a call costs the CPU - validation, argument
+    marshalling and the kernel launches - not the kernels, which run after the call has
+    returned.  The wrapping itself adds two clock reads per call."""
+
+    _NAMES = ("kv_write", "qk_norm_rope_kv_write", "paged_decode", "prefill", "prefill_paged")
+
+    def __init__(self):
+        self.calls: Dict[str, List[float]] = {n: [0, 0.0] for n in self._NAMES}
+
+    def _wrap(self, name, fn):
+        acc = self.calls[name]
+        clock = time.perf_counter
+
+        def timed(*args, **kwargs):
+            t0 = clock()
+            r = fn(*args, **kwargs)
+            acc[1] += clock() - t0
+            acc[0] += 1
+            return r
+        return timed
+
+    def __enter__(self):
+        self._saved = {n: getattr(ops, n) for n in self._NAMES}
+        for n in self._NAMES:
+            setattr(ops, n, self._wrap(n, self._saved[n]))
+        return self
+
+    def __exit__(self, *exc):
+        for n, fn in self._saved.items():
+            setattr(ops, n, fn)
+        return False
+
+    def per_call_us(self) -> Dict[str, Dict[str, float]]:
+        return {n: {"calls": int(c), "host_us_per_call": round(t / c * 1e6, 2)}
+                for n, (c, t) in self.calls.items() if c}
+
+
 def main() -> int:
     import argparse
     import json

@@ -26,24 +26,56 @@ def _dtype_code(t: torch.Tensor, allowed=(torch.bfloat16, torch.float32)) -> int
 
 
 def _require_gpu(*tensors: torch.Tensor) -> torch.device:
-    dev = tensors[0].device
+    idx = tensors[0].get_device()
     for t in tensors:
-        if t.device.type != "cuda":
+        i = t.get_device()
+        if i < 0:
             raise ValueError(
                 f"attention kernels run on the GPU only; got a tensor on {t.device}"
             )
-        if t.device != dev:
-            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
-    return dev
+        if i != idx:
+            raise ValueError(f"tensors on different devices: {tensors[0].device} and {t.device}")
+    return tensors[0].device
+
+
+def _raw_stream(index: int) -> int:
+    """The current HIP stream of device ``index`` as an integer handle."""
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
 
 
 def _last_contig(name: str, t: torch.Tensor) -> None:
     if t.stride(-1) != 1:
         raise ValueError(f"{name} must have a contiguous last dimension")
+
+
+class TensorMemo:
+    """Results derived from a tensor by reading it back to the host, kept while the same
+    tensor object comes back unmodified (same version counter), so that the layers of a
+    step which share one attention mask or one cu_seqlens tensor synchronise with the
+    device once instead of once per layer.  Holds strong references to the last
+    ``size`` tensors (masks and cu_seqlens: small), so that a freed tensor's memory and
+    id cannot come back as a different tensor with a stale result."""
+
+    def __init__(self, size: int = 8):
+        self.size = size
+        self._items: list = []
+
+    def get(self, t: torch.Tensor, key):
+        for item in self._items:
+            if item[0] is t and item[1] == t._version and item[2] == key:
+                return item[3]
+        return None
+
+    def put(self, t: torch.Tensor, key, value) -> None:
+        self._items.insert(0, (t, t._version, key, value))
+        del self._items[self.size:]
+
+
+_MAX_SEQLEN = TensorMemo()
 
 
 def _default_scale(head_dim: int, scale: Optional[float]) -> float:
@@ -202,8 +234,13 @@ def decode_workspace(device: torch.device, nbytes: int, stream=None) -> torch.Te
     """A decode workspace of at least ``nbytes`` for (``device``, ``stream``) (default: the
     device's current stream), cached and reused by later calls on that stream."""
     dev = torch.device(device)
-    st = torch.cuda.current_stream(dev) if stream is None else stream
-    key = (dev, st.cuda_stream)
+    if stream is not None:
+        handle = stream.cuda_stream
+    elif dev.type == "cuda":
+        handle = _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+    else:
+        handle = 0
+    key = (dev.index if dev.type == "cuda" else -1, handle)
     ws = _DECODE_WS.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
@@ -211,6 +248,73 @@ def decode_workspace(device: torch.device, nbytes: int, stream=None) -> torch.Te
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _DECODE_WS[key] = ws
     return ws
+
+
+class _DecodePlan:
+    """What paged_decode validated and derived for one signature of its arguments
+    (shapes, strides, dtypes, devices), so that a repeated call only reads pointers."""
+
+    __slots__ = ("squeeze", "b", "h", "d", "hkv", "bs", "nb", "max_blocks", "dt", "fp8",
+                 "scale", "need", "bt_copy", "ctx_copy", "out_shape", "out_dtype")
+
+
+_DECODE_PLANS: dict = {}
+_PLAN_CACHE_MAX = 256
+
+
+def _decode_plan(q, k_cache, v_cache, block_tables, context_lens, scale, out, k_scale,
+                 v_scale) -> _DecodePlan:
+    """Full validation of a paged_decode call (raises ValueError on a bad one)."""
+    _require_gpu(q, k_cache, v_cache, block_tables, context_lens)
+    squeeze = q.dim() == 4
+    if squeeze:
+        if q.shape[1] != 1:
+            raise ValueError("paged_decode takes one query token per sequence")
+        q3 = q[:, 0]
+    elif q.dim() == 3:
+        q3 = q
+    else:
+        raise ValueError(f"q must be (B, H, D) or (B, 1, H, D), got {tuple(q.shape)}")
+    b, h, d = q3.shape
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, head_dim]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache layer slices must be contiguous")
+    nb, hkv, bs, dc = k_cache.shape
+    if dc != d:
+        raise ValueError(f"head_dim mismatch: q {d}, cache {dc}")
+    if h % hkv != 0:
+        raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
+    fp8 = is_fp8_cache(k_cache)
+    if fp8:
+        if v_cache.dtype != k_cache.dtype or q3.dtype != torch.bfloat16:
+            raise ValueError("fp8 caches take bf16 queries (and share one dtype)")
+        _fp8_scales(k_cache, k_scale, v_scale)
+    elif not (q3.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("q and the caches must share one dtype")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise ValueError("block_tables must be (B, max_blocks) int32")
+    if context_lens.dtype != torch.int64 or context_lens.shape != (b,):
+        raise ValueError("context_lens must be (B,) int64")
+    _last_contig("q", q3)
+    if out is not None:
+        out3 = out[:, 0] if out.dim() == 4 else out
+        if out3.shape != (b, h, d) or out3.dtype != q3.dtype:
+            raise ValueError("out must match q's shape and dtype")
+        if out.get_device() != q.get_device():
+            raise ValueError("out must be on q's device")
+        _last_contig("out", out3)
+    max_blocks = block_tables.shape[1]
+    check_decode_shape(d, bs, h, hkv, q3.dtype, fp8)
+    pl = _DecodePlan()
+    pl.squeeze, pl.b, pl.h, pl.d, pl.hkv, pl.bs, pl.nb = squeeze, b, h, d, hkv, bs, nb
+    pl.max_blocks, pl.dt, pl.fp8 = max_blocks, _dtype_code(q3), fp8
+    pl.scale = _default_scale(d, scale)
+    pl.need = decode_workspace_bytes(b, h, hkv, max_blocks, bs, d, q3.dtype)
+    pl.bt_copy = block_tables.stride(1) != 1
+    pl.ctx_copy = not context_lens.is_contiguous()
+    pl.out_shape, pl.out_dtype = (b, h, d), q3.dtype
+    return pl
 
 
 def paged_decode(
@@ -235,82 +339,75 @@ def paged_decode(
     default the cached one of the current stream (``decode_workspace``) is used.
     fp8 caches (uint8 / float8_e4m3fn codes) take their per-row ``k_scale`` /
     ``v_scale`` [num_blocks, H_kv, BS] float32 and bf16 queries.
+
+    A call is validated in full the first time its arguments' shapes, strides, dtypes
+    and devices are seen; later calls with the same signature reuse that result.
     """
-    dev = _require_gpu(q, k_cache, v_cache, block_tables, context_lens)
-    squeeze = q.dim() == 4
-    if squeeze:
-        if q.shape[1] != 1:
-            raise ValueError("paged_decode takes one query token per sequence")
-        q3 = q[:, 0]
-    elif q.dim() == 3:
-        q3 = q
+    sig = (q.shape, q.stride(), q.dtype, q.get_device(),
+           k_cache.shape, k_cache.stride(), k_cache.dtype, k_cache.get_device(),
+           v_cache.shape, v_cache.stride(), v_cache.dtype, v_cache.get_device(),
+           block_tables.shape, block_tables.stride(), block_tables.dtype,
+           block_tables.get_device(),
+           context_lens.shape, context_lens.stride(), context_lens.dtype,
+           context_lens.get_device(), scale,
+           None if out is None else (out.shape, out.stride(), out.dtype),
+           None if k_scale is None else (k_scale.shape, k_scale.stride(), k_scale.dtype,
+                                         k_scale.get_device()),
+           None if v_scale is None else (v_scale.shape, v_scale.stride(), v_scale.dtype,
+                                         v_scale.get_device()))
+    pl = _DECODE_PLANS.get(sig)
+    if pl is None:
+        pl = _decode_plan(q, k_cache, v_cache, block_tables, context_lens, scale, out,
+                          k_scale, v_scale)
+        if len(_DECODE_PLANS) >= _PLAN_CACHE_MAX:
+            _DECODE_PLANS.clear()
+        _DECODE_PLANS[sig] = pl
+    q3 = q[:, 0] if pl.squeeze else q
+    dev_index = q.get_device()
+    stream = _raw_stream(dev_index)
+    if workspace is None:
+        ws = _DECODE_WS.get((dev_index, stream))
+        if ws is None or ws.numel() < pl.need:
+            ws = decode_workspace(q.device, pl.need)
     else:
-        raise ValueError(f"q must be (B, H, D) or (B, 1, H, D), got {tuple(q.shape)}")
-    b, h, d = q3.shape
-    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
-        raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, head_dim]")
-    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-        raise ValueError("k_cache/v_cache layer slices must be contiguous")
-    nb, hkv, bs, dc = k_cache.shape
-    if dc != d:
-        raise ValueError(f"head_dim mismatch: q {d}, cache {dc}")
-    if h % hkv != 0:
-        raise ValueError(f"num_heads must be divisible by num_kv_heads, got {h=} and {hkv=}")
-    fp8 = is_fp8_cache(k_cache)
-    if fp8:
-        if v_cache.dtype != k_cache.dtype or q3.dtype != torch.bfloat16:
-            raise ValueError("fp8 caches take bf16 queries (and share one dtype)")
-        k_scale, v_scale = _fp8_scales(k_cache, k_scale, v_scale)
-    elif not (q3.dtype == k_cache.dtype == v_cache.dtype):
-        raise ValueError("q and the caches must share one dtype")
-    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.shape[0] != b:
-        raise ValueError("block_tables must be (B, max_blocks) int32")
-    if context_lens.dtype != torch.int64 or context_lens.shape != (b,):
-        raise ValueError("context_lens must be (B,) int64")
-    if block_tables.stride(1) != 1:
-        block_tables = block_tables.contiguous()
-    context_lens = context_lens.contiguous()
-    dt = _dtype_code(q3)
-    _last_contig("q", q3)
+        ws = workspace
+        if ws.numel() * ws.element_size() < pl.need:
+            raise ValueError(f"decode workspace of {ws.numel() * ws.element_size()} bytes, "
+                             f"{pl.need} needed")
+    ws_bytes = ws.numel() * ws.element_size()
     if out is None:
-        out3 = torch.empty((b, h, d), dtype=q3.dtype, device=dev)
+        out3 = torch.empty(pl.out_shape, dtype=pl.out_dtype, device=q.device)
     else:
         out3 = out[:, 0] if out.dim() == 4 else out
-        if out3.shape != (b, h, d) or out3.dtype != q3.dtype:
-            raise ValueError("out must match q's shape and dtype")
-        _last_contig("out", out3)
-    max_blocks = block_tables.shape[1]
-    check_decode_shape(d, bs, h, hkv, q3.dtype, fp8)
-    need = decode_workspace_bytes(b, h, hkv, max_blocks, bs, d, q3.dtype)
-    if workspace is None:
-        workspace = decode_workspace(dev, need)
-    ws_bytes = workspace.numel() * workspace.element_size()
-    if ws_bytes < need:
-        raise ValueError(f"decode workspace of {ws_bytes} bytes, {need} needed")
-    ws_ptr = workspace.data_ptr()
+    if pl.bt_copy:
+        block_tables = block_tables.contiguous()
+    if pl.ctx_copy:
+        context_lens = context_lens.contiguous()
     lib = _lib.load()
-    if fp8:
+    q_st, o_st = q3.stride(), out3.stride()
+    if pl.fp8:
         st = lib.nia_paged_decode_fp8(
-            out3.data_ptr(), out3.stride(0), out3.stride(1),
-            q3.data_ptr(), q3.stride(0), q3.stride(1),
+            out3.data_ptr(), o_st[0], o_st[1], q3.data_ptr(), q_st[0], q_st[1],
             k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
-            block_tables.data_ptr(), block_tables.stride(0), max_blocks, context_lens.data_ptr(),
-            b, h, hkv, d, bs, nb, _default_scale(d, scale), ws_ptr, ws_bytes, _stream(dev),
+            block_tables.data_ptr(), block_tables.stride(0), pl.max_blocks,
+            context_lens.data_ptr(), pl.b, pl.h, pl.hkv, pl.d, pl.bs, pl.nb, pl.scale,
+            ws.data_ptr(), ws_bytes, stream,
         )
-        _lib.check("nia_paged_decode_fp8", st)
+        if st:
+            _lib.check("nia_paged_decode_fp8", st)
     else:
         st = lib.nia_paged_decode(
-            out3.data_ptr(), out3.stride(0), out3.stride(1),
-            q3.data_ptr(), q3.stride(0), q3.stride(1),
+            out3.data_ptr(), o_st[0], o_st[1], q3.data_ptr(), q_st[0], q_st[1],
             k_cache.data_ptr(), v_cache.data_ptr(),
-            block_tables.data_ptr(), block_tables.stride(0), max_blocks,
-            context_lens.data_ptr(), b, h, hkv, d, bs, nb, _default_scale(d, scale), ws_ptr,
-            ws_bytes, dt, _stream(dev),
+            block_tables.data_ptr(), block_tables.stride(0), pl.max_blocks,
+            context_lens.data_ptr(), pl.b, pl.h, pl.hkv, pl.d, pl.bs, pl.nb, pl.scale,
+            ws.data_ptr(), ws_bytes, pl.dt, stream,
         )
-        _lib.check("nia_paged_decode", st)
+        if st:
+            _lib.check("nia_paged_decode", st)
     if out is not None:
         return out
-    return out3.unsqueeze(1) if squeeze else out3
+    return out3.unsqueeze(1) if pl.squeeze else out3
 
 
 # ---------------------------------------------------------------------------------
@@ -321,6 +418,8 @@ def paged_decode(
 def _i32(name: str, t: torch.Tensor, n: int) -> torch.Tensor:
     if t.dim() != 1 or t.shape[0] != n:
         raise ValueError(f"{name} must be ({n},)")
+    if t.dtype == torch.int32 and t.stride(0) == 1:
+        return t
     return t.to(torch.int32).contiguous()
 
 
@@ -395,16 +494,24 @@ def varlen_attention(
 
     Chunk i owns rows cu_seqlens[i] .. cu_seqlens[i+1]; causal=True aligns the
     mask top-left (equal q/k lengths in the prefill case).  ``max_seqlen_q``
-    sizes the launch grid; when omitted it is read back from the device.
+    sizes the launch grid.  When it is omitted it is computed from cu_seqlens_q:
+    on the host for a CPU tensor, else read back from the device once per
+    cu_seqlens tensor (the blocks of a vision tower share one, see TensorMemo).
+    cu_seqlens on the CPU are copied to q's device.
     """
     if cu_seqlens_k is None:
         cu_seqlens_k = cu_seqlens_q
-    cq = cu_seqlens_q.to(torch.int32)
-    ck = cu_seqlens_k.to(torch.int32)
-    lq = cq[1:] - cq[:-1]
-    lk = ck[1:] - ck[:-1]
     if max_seqlen_q is None:
-        max_seqlen_q = int(lq.max().item()) if lq.numel() else 0
+        max_seqlen_q = _MAX_SEQLEN.get(cu_seqlens_q, "max")
+        if max_seqlen_q is None:
+            lens = cu_seqlens_q[1:] - cu_seqlens_q[:-1]
+            max_seqlen_q = int(lens.max().item()) if lens.numel() else 0
+            _MAX_SEQLEN.put(cu_seqlens_q, "max", max_seqlen_q)
+    cq = cu_seqlens_q.to(device=q.device, dtype=torch.int32)
+    ck = cq if cu_seqlens_k is cu_seqlens_q else \
+        cu_seqlens_k.to(device=q.device, dtype=torch.int32)
+    lq = cq[1:] - cq[:-1]
+    lk = lq if ck is cq else ck[1:] - ck[:-1]
     return prefill(q, k, v, cq[:-1], lq, ck[:-1], lk, max_seqlen_q,
                    CAUSAL_TOP_LEFT if causal else CAUSAL_NONE, scale, out)
 
@@ -524,6 +631,97 @@ def _prefill_paged_fp8(q, k_cache, v_cache, block_tables, q_start, q_len, contex
 # ---------------------------------------------------------------------------------
 
 
+class _QkPlan:
+    """What qk_norm_rope_kv_write validated and derived for one argument signature."""
+
+    __slots__ = ("n", "h", "hkv", "d", "q_tok", "q_head", "k_tok", "k_head", "v_tok",
+                 "v_head", "v_copy", "num_axes", "sec0", "sec1", "pos_copy", "inv_copy", "w_copy",
+                 "slot_copy", "write", "fp8", "bs", "nb", "dt", "eps")
+
+
+_QK_PLANS: dict = {}
+
+
+def _qk_plan(q, k, v, q_norm_weight, k_norm_weight, eps, positions, inv_freq, mrope_section,
+             k_cache, v_cache, slot_mapping, k_scale, v_scale) -> _QkPlan:
+    """Full validation of a qk_norm_rope_kv_write call (raises ValueError on a bad one)."""
+    _require_gpu(q, k, v, positions, inv_freq)
+    d = q.shape[-1]
+    if k.shape[-1] != d or v.shape != k.shape or q.shape[:-2] != k.shape[:-2]:
+        raise ValueError("q (..., H, D), k and v (..., H_kv, D) with the same leading dims")
+    if (q_norm_weight is None) != (k_norm_weight is None):
+        raise ValueError("q and k norm weights must both be given or both be None")
+    dt = _dtype_code(q)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k and v must share one dtype")
+    lead = q.shape[:-2]
+    n = math.prod(lead)
+    try:  # q and k are updated in place, so they must be viewable as (tokens, heads, D)
+        q2 = q.view(n, q.shape[-2], d)
+        k2 = k.view(n, k.shape[-2], d)
+    except RuntimeError as e:
+        raise ValueError(f"q and k must be viewable as (tokens, heads, D): {e}") from None
+    try:  # v is only read: one that is not viewable is copied for each call
+        v2 = v.view(n, v.shape[-2], d)
+        v_copy = False
+    except RuntimeError:
+        v2 = v.reshape(n, v.shape[-2], d)
+        v_copy = True
+    for name, t in (("q", q2), ("k", k2), ("v", v2)):
+        _last_contig(name, t)
+    pl = _QkPlan()
+    if mrope_section is None:
+        if positions.shape != lead:
+            raise ValueError(f"positions must have shape {tuple(lead)}")
+        pl.num_axes, pl.sec0, pl.sec1 = 1, 0, 0
+    else:
+        if positions.shape != (3, *lead):
+            raise ValueError(f"mRoPE positions must have shape (3, {tuple(lead)})")
+        pl.num_axes, pl.sec0, pl.sec1 = 3, int(mrope_section[0]), int(mrope_section[1])
+    pl.pos_copy = positions.dtype != torch.int64 or not positions.is_contiguous()
+    if not inv_freq.is_floating_point() or inv_freq.numel() != d // 2:
+        raise ValueError(f"inv_freq must be a ({d // 2},) floating-point table")
+    # A module cast to the model dtype holds a rounded table; the products
+    # position * inv_freq are still formed in fp32 from those rounded values.
+    pl.inv_copy = inv_freq.dtype != torch.float32 or not inv_freq.is_contiguous()
+    pl.w_copy = False
+    if q_norm_weight is not None:
+        if q_norm_weight.shape != (d,) or k_norm_weight.shape != (d,) or \
+                q_norm_weight.dtype != q.dtype or k_norm_weight.dtype != q.dtype:
+            raise ValueError(f"norm weights must be ({d},) in the model dtype")
+        if q_norm_weight.get_device() != q.get_device() or \
+                k_norm_weight.get_device() != q.get_device():
+            raise ValueError("norm weights must be on q's device")
+        pl.w_copy = not (q_norm_weight.is_contiguous() and k_norm_weight.is_contiguous())
+    pl.write, pl.fp8, pl.bs, pl.nb, pl.slot_copy = False, False, 1, 0, False
+    if k_cache is not None:
+        if v_cache is None or slot_mapping is None:
+            raise ValueError("a cache write needs v_cache and slot_mapping")
+        _require_gpu(q, k_cache, v_cache, slot_mapping)
+        if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or \
+                k_cache.shape[1] != k2.shape[1] or k_cache.shape[3] != d:
+            raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, D]")
+        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+            raise ValueError("k_cache/v_cache layer slices must be contiguous")
+        pl.fp8 = is_fp8_cache(k_cache)
+        if pl.fp8:
+            if v_cache.dtype != k_cache.dtype:
+                raise ValueError("k_cache and v_cache must share one dtype")
+            _fp8_scales(k_cache, k_scale, v_scale)
+        elif k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+            raise ValueError("caches must share the model dtype")
+        if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
+            raise ValueError(f"slot_mapping must be int64 with {n} entries")
+        pl.slot_copy = not slot_mapping.is_contiguous()
+        pl.write, pl.nb, pl.bs = True, k_cache.shape[0], k_cache.shape[2]
+    pl.n, pl.h, pl.hkv, pl.d, pl.dt, pl.eps = n, q2.shape[1], k2.shape[1], d, dt, float(eps)
+    pl.q_tok, pl.q_head = q2.stride(0), q2.stride(1)
+    pl.k_tok, pl.k_head = k2.stride(0), k2.stride(1)
+    pl.v_tok, pl.v_head = v2.stride(0), v2.stride(1)
+    pl.v_copy = v_copy
+    return pl
+
+
 def qk_norm_rope_kv_write(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -550,81 +748,61 @@ def qk_norm_rope_kv_write(
     positions: the leading dims' position ids, or (3, *leading) for mRoPE with
     ``mrope_section``; inv_freq: (64,) (any float dtype); norm weights (128,) or None (no QK
     norm; both or neither); caches one layer [num_blocks, H_kv, BS, 128] or None.
+    A call is validated in full the first time its arguments' shapes, strides, dtypes and
+    devices are seen; later calls with the same signature reuse that result.
     """
-    dev = _require_gpu(q, k, v, positions, inv_freq)
-    d = q.shape[-1]
-    if k.shape[-1] != d or v.shape != k.shape or q.shape[:-2] != k.shape[:-2]:
-        raise ValueError("q (..., H, D), k and v (..., H_kv, D) with the same leading dims")
-    if (q_norm_weight is None) != (k_norm_weight is None):
-        raise ValueError("q and k norm weights must both be given or both be None")
-    dt = _dtype_code(q)
-    if not (q.dtype == k.dtype == v.dtype):
-        raise ValueError("q, k and v must share one dtype")
-    lead = q.shape[:-2]
-    n = math.prod(lead)
-    try:  # q and k are updated in place, so they must be viewable as (tokens, heads, D)
-        q2 = q.view(n, q.shape[-2], d)
-        k2 = k.view(n, k.shape[-2], d)
-    except RuntimeError as e:
-        raise ValueError(f"q and k must be viewable as (tokens, heads, D): {e}") from None
-    v2 = v.reshape(n, v.shape[-2], d)
-    for name, t in (("q", q2), ("k", k2), ("v", v2)):
-        _last_contig(name, t)
-    if mrope_section is None:
-        if positions.shape != lead:
-            raise ValueError(f"positions must have shape {tuple(lead)}")
-        num_axes, sec0, sec1 = 1, 0, 0
-    else:
-        if positions.shape != (3, *lead):
-            raise ValueError(f"mRoPE positions must have shape (3, {tuple(lead)})")
-        num_axes, sec0, sec1 = 3, int(mrope_section[0]), int(mrope_section[1])
-    pos = positions.reshape(num_axes, n).to(torch.int64).contiguous()
-    if not inv_freq.is_floating_point() or inv_freq.numel() != d // 2:
-        raise ValueError(f"inv_freq must be a ({d // 2},) floating-point table")
-    # A module cast to the model dtype holds a rounded table; the products
-    # position * inv_freq are still formed in fp32 from those rounded values.
-    inv = inv_freq.to(torch.float32).contiguous()
-    qw = kw = None
-    if q_norm_weight is not None:
-        if q_norm_weight.shape != (d,) or k_norm_weight.shape != (d,) or \
-                q_norm_weight.dtype != q.dtype or k_norm_weight.dtype != q.dtype:
-            raise ValueError(f"norm weights must be ({d},) in the model dtype")
-        qw, kw = q_norm_weight.contiguous(), k_norm_weight.contiguous()
+    nw = q_norm_weight is not None
+    sig = (q.shape, q.stride(), q.dtype, q.get_device(), k.shape, k.stride(), k.dtype,
+           k.get_device(), v.shape, v.stride(), v.dtype, v.get_device(),
+           (q_norm_weight.shape, q_norm_weight.stride(), q_norm_weight.dtype,
+            q_norm_weight.get_device()) if nw else None,
+           (k_norm_weight.shape, k_norm_weight.stride(), k_norm_weight.dtype,
+            k_norm_weight.get_device()) if k_norm_weight is not None else None,
+           eps, positions.shape, positions.stride(), positions.dtype, positions.get_device(),
+           inv_freq.shape, inv_freq.stride(), inv_freq.dtype, inv_freq.get_device(),
+           mrope_section,
+           (k_cache.shape, k_cache.stride(), k_cache.dtype, k_cache.get_device())
+           if k_cache is not None else None,
+           (v_cache.shape, v_cache.stride(), v_cache.dtype, v_cache.get_device())
+           if v_cache is not None else None,
+           (slot_mapping.shape, slot_mapping.stride(), slot_mapping.dtype,
+            slot_mapping.get_device()) if slot_mapping is not None else None,
+           (k_scale.shape, k_scale.stride(), k_scale.dtype, k_scale.get_device())
+           if k_scale is not None else None,
+           (v_scale.shape, v_scale.stride(), v_scale.dtype, v_scale.get_device())
+           if v_scale is not None else None)
+    pl = _QK_PLANS.get(sig)
+    if pl is None:
+        pl = _qk_plan(q, k, v, q_norm_weight, k_norm_weight, eps, positions, inv_freq,
+                      mrope_section, k_cache, v_cache, slot_mapping, k_scale, v_scale)
+        if len(_QK_PLANS) >= _PLAN_CACHE_MAX:
+            _QK_PLANS.clear()
+        _QK_PLANS[sig] = pl
+    pos = positions.to(torch.int64).contiguous() if pl.pos_copy else positions
+    inv = inv_freq.to(torch.float32).contiguous() if pl.inv_copy else inv_freq
+    qw, kw = q_norm_weight, k_norm_weight
+    if pl.w_copy:
+        qw, kw = qw.contiguous(), kw.contiguous()
+    if pl.v_copy:
+        v = v.reshape(pl.n, pl.hkv, pl.d)
     kc_ptr = vc_ptr = sl_ptr = None
-    bs, nb = 1, 0
-    keep = []
-    if k_cache is not None:
-        if v_cache is None or slot_mapping is None:
-            raise ValueError("a cache write needs v_cache and slot_mapping")
-        if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or \
-                k_cache.shape[1] != k2.shape[1] or k_cache.shape[3] != d:
-            raise ValueError("k_cache/v_cache must be [num_blocks, H_kv, block_size, D]")
-        if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-            raise ValueError("k_cache/v_cache layer slices must be contiguous")
-        fp8 = is_fp8_cache(k_cache)
-        if fp8:
-            if v_cache.dtype != k_cache.dtype:
-                raise ValueError("k_cache and v_cache must share one dtype")
-            k_scale, v_scale = _fp8_scales(k_cache, k_scale, v_scale)
-        elif k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
-            raise ValueError("caches must share the model dtype")
-        if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
-            raise ValueError(f"slot_mapping must be int64 with {n} entries")
-        slots = slot_mapping.reshape(-1).contiguous()
-        keep.append(slots)
-        nb, bs = k_cache.shape[0], k_cache.shape[2]
+    if pl.write:
+        slots = slot_mapping.contiguous() if pl.slot_copy else slot_mapping
         kc_ptr, vc_ptr, sl_ptr = k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr()
     lib = _lib.load()
-    args = (q2.data_ptr(), q2.stride(0), q2.stride(1), k2.data_ptr(), k2.stride(0), k2.stride(1),
-            v2.data_ptr(), v2.stride(0), v2.stride(1),
-            qw.data_ptr() if qw is not None else None, kw.data_ptr() if kw is not None else None,
-            float(eps), pos.data_ptr(), pos.stride(0), num_axes, inv.data_ptr(), sec0, sec1,
+    args = (q.data_ptr(), pl.q_tok, pl.q_head, k.data_ptr(), pl.k_tok, pl.k_head,
+            v.data_ptr(), pl.v_tok, pl.v_head,
+            qw.data_ptr() if nw else None, kw.data_ptr() if nw else None,
+            pl.eps, pos.data_ptr(), pl.n, pl.num_axes, inv.data_ptr(), pl.sec0, pl.sec1,
             kc_ptr, vc_ptr)
-    tail = (sl_ptr, n, q2.shape[1], k2.shape[1], d, bs, nb, dt, _stream(dev))
-    if k_cache is not None and is_fp8_cache(k_cache):
+    tail = (sl_ptr, pl.n, pl.h, pl.hkv, pl.d, pl.bs, pl.nb, pl.dt,
+            _raw_stream(q.get_device()))
+    if pl.fp8:
         st = lib.nia_qk_norm_rope_kv_write_fp8(*args, k_scale.data_ptr(), v_scale.data_ptr(),
                                                *tail)
-        _lib.check("nia_qk_norm_rope_kv_write_fp8", st)
+        if st:
+            _lib.check("nia_qk_norm_rope_kv_write_fp8", st)
         return
     st = lib.nia_qk_norm_rope_kv_write(*args, *tail)
-    _lib.check("nia_qk_norm_rope_kv_write", st)
+    if st:
+        _lib.check("nia_qk_norm_rope_kv_write", st)

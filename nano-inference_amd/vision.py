@@ -58,8 +58,7 @@ class VisionAttention(VisionAttentionBase):
         qkv = self.qkv(x).reshape(seq_len, 3, self.num_heads, self.head_dim)
         q, k, v = qkv.permute(1, 0, 2, 3).unbind(0)
         q, k = apply_rotary_pos_emb_vision(q, k, cos, sin)
-        out = ops.varlen_attention(q, k, v, cu_seqlens.to(x.device), max_seqlen_q=max_seqlen,
-                                   causal=False)
+        out = ops.varlen_attention(q, k, v, cu_seqlens, max_seqlen_q=max_seqlen, causal=False)
         return self.proj(out.reshape(seq_len, self.num_heads * self.head_dim))
 
 
