@@ -71,6 +71,42 @@ def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int,
     return lens
 
 
+_INDEX_CACHE: dict = {}
+
+
+def _seq_index(b: int, q_step: int, q_len: int, k_step: int, k_len: int,
+               device: torch.device):
+    """(q_start, q_len, k_start, k_len) int32 tensors for b equal sequences, built once
+    per shape and device (the kernels only read them)."""
+    key = (b, q_step, q_len, k_step, k_len, device)
+    t = _INDEX_CACHE.get(key)
+    if t is None:
+        ar = torch.arange(b, dtype=torch.int32)
+        t = tuple(x.to(device) for x in (ar * q_step, torch.full((b,), q_len, dtype=torch.int32),
+                                          ar * k_step, torch.full((b,), k_len, dtype=torch.int32)))
+        if len(_INDEX_CACHE) >= 64:
+            _INDEX_CACHE.clear()
+        _INDEX_CACHE[key] = t
+    return t
+
+
+def _token_rows(x: torch.Tensor):
+    """A (B, H, S, D) tensor as token rows without a copy: (view (rows, H, D), step) with
+    token s of batch b at row b * step + s, or None when its strides do not allow it.
+    Both the (B, H, S, D) layout and a transposed (B, S, H, D) one do."""
+    bb, hh, ss, dd = x.shape
+    sb, sh, st, sd = x.stride()
+    if sd != 1 or bb == 0 or ss == 0:
+        return None
+    if ss == 1:
+        st = sb if bb > 1 else dd  # the stride of a size-1 dimension is arbitrary
+    if st <= 0 or (bb > 1 and sb % st):
+        return None
+    step = sb // st if bb > 1 else 0
+    rows = (bb - 1) * step + ss
+    return x.as_strided((rows, hh, dd), (st, sh, 1)), step
+
+
 def scaled_dot_product_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -83,7 +119,8 @@ def scaled_dot_product_attention(
     Shapes as in src/nano_inference/layers/attention.py:12-50: q (B, H, S_q, D),
     k, v (B, H_kv, S_k, D) (H_kv may divide H), output (B, H, S_q, D).  As in the
     reference the causal mask is applied only when S_q == S_k; the padding mask
-    is sliced to S_k.
+    is sliced to S_k.  q, k and v are read in place (their (B, H, S, D) strides become
+    per-sequence row offsets), and the output is written in q's layout.
     """
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be (B, H, S, D)")
@@ -91,18 +128,21 @@ def scaled_dot_product_attention(
     sk = k.shape[2]
     causal = ops.CAUSAL_TOP_LEFT if (is_causal and sq == sk) else ops.CAUSAL_NONE
     dev = q.device
-    # (B, H, S, D) -> token-major views (B*S, H, D) when the strides allow it.
-    q3 = q.transpose(1, 2).reshape(b * sq, h, d)
-    k3 = k.transpose(1, 2).reshape(b * sk, k.shape[1], d)
-    v3 = v.transpose(1, 2).reshape(b * sk, v.shape[1], d)
-    ar = torch.arange(b, device=dev, dtype=torch.int32)
-    q_len = torch.full((b,), sq, device=dev, dtype=torch.int32)
+    out = torch.empty_like(q)
+    rq, rk, rv, ro = (_token_rows(t) for t in (q, k, v, out))
+    if rq and rk and rv and ro and rk[1] == rv[1] and ro[1] == rq[1]:
+        (q3, q_step), (k3, k_step), (v3, _), (o3, _) = rq, rk, rv, ro
+    else:  # other layouts: token-major copies
+        q3 = q.transpose(1, 2).reshape(b * sq, h, d)
+        k3 = k.transpose(1, 2).reshape(b * sk, k.shape[1], d)
+        v3 = v.transpose(1, 2).reshape(b * sk, v.shape[1], d)
+        out = torch.empty(b, sq, h, d, dtype=q.dtype, device=dev).transpose(1, 2)
+        o3, q_step, k_step = out.transpose(1, 2).view(b * sq, h, d), sq, sk
+    q_start, q_len, k_start, k_len = _seq_index(b, q_step, sq, k_step, sk, dev)
     if attention_mask is not None:
         k_len = _prefix_lengths(attention_mask, b, sk, dev)
-    else:
-        k_len = torch.full((b,), sk, device=dev, dtype=torch.int32)
-    out = ops.prefill(q3, k3, v3, ar * sq, q_len, ar * sk, k_len, sq, causal)
-    return out.view(b, sq, h, d).transpose(1, 2)
+    ops.prefill(q3, k3, v3, q_start, q_len, k_start, k_len, sq, causal, out=o3)
+    return out
 
 
 class CausalSelfAttentionBase(nn.Module):
@@ -202,9 +242,9 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         """No-cache path (metadata None): causal attention over the step's K/V."""
         b, s = q.shape[:2]
         dev = q.device
-        ar = torch.arange(b, device=dev, dtype=torch.int32) * s
-        lens = torch.full((b,), s, device=dev, dtype=torch.int32)
-        k_len = lens if attention_mask is None else _prefix_lengths(attention_mask, b, s, dev)
+        ar, lens, _, k_len = _seq_index(b, s, s, s, s, dev)
+        if attention_mask is not None:
+            k_len = _prefix_lengths(attention_mask, b, s, dev)
         return ops.prefill(
             q.reshape(b * s, self.num_heads, self.head_dim),
             k.reshape(b * s, self.num_kv_heads, self.head_dim),

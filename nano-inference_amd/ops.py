@@ -507,13 +507,23 @@ def varlen_attention(
             lens = cu_seqlens_q[1:] - cu_seqlens_q[:-1]
             max_seqlen_q = int(lens.max().item()) if lens.numel() else 0
             _MAX_SEQLEN.put(cu_seqlens_q, "max", max_seqlen_q)
-    cq = cu_seqlens_q.to(device=q.device, dtype=torch.int32)
-    ck = cq if cu_seqlens_k is cu_seqlens_q else \
-        cu_seqlens_k.to(device=q.device, dtype=torch.int32)
-    lq = cq[1:] - cq[:-1]
-    lk = lq if ck is cq else ck[1:] - ck[:-1]
-    return prefill(q, k, v, cq[:-1], lq, ck[:-1], lk, max_seqlen_q,
+    sq, lq = _starts_and_lengths(cu_seqlens_q, q.device)
+    sk, lk = (sq, lq) if cu_seqlens_k is cu_seqlens_q else \
+        _starts_and_lengths(cu_seqlens_k, q.device)
+    return prefill(q, k, v, sq, lq, sk, lk, max_seqlen_q,
                    CAUSAL_TOP_LEFT if causal else CAUSAL_NONE, scale, out)
+
+
+def _starts_and_lengths(cu: torch.Tensor, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """int32 chunk starts and lengths on ``device`` from cumulative lengths, derived once
+    per cu_seqlens tensor."""
+    key = ("starts", device)
+    got = _MAX_SEQLEN.get(cu, key)
+    if got is None:
+        c = cu.to(device=device, dtype=torch.int32)
+        got = (c[:-1], c[1:] - c[:-1])
+        _MAX_SEQLEN.put(cu, key, got)
+    return got
 
 
 # ---------------------------------------------------------------------------------
