@@ -17,13 +17,15 @@ causal prefill TFLOP/s against bf16 MFMA peak (2.5 PFLOP/s dense), the other
 synthetic workloads, and the reference's CPU attention timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       python bench.py --profile-decode N   (only N decode steps plus a 1 GiB copy,
-                                             for rocprofv3 counter runs)
-       python bench.py --profile-prefill N  (only N causal prefill launches)
+       python bench.py --profile WORKLOAD [--launches N]
+           (three 1 GiB copies, then N launches of one workload, for rocprofv3 counter
+            runs; WORKLOAD: decode, decode_vl, decode_fp8, kv_write, kv_write_prefill,
+            prefill, chunked, vision_full, vision_window)
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -108,20 +110,39 @@ def graph_call_ms(torch, fn, calls: int = 50, rounds: int = 5) -> float:
     return sorted(times)[len(times) // 2]
 
 
-def read_traffic(workload: str):
-    """Per-launch HBM bytes of the decode kernels from a committed counter summary."""
+def source_digest(paths) -> str:
+    """sha256 of the kernel sources a counter summary was measured on."""
+    h = hashlib.sha256()
+    for rel in paths:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+DECODE_SOURCES = ("nano-inference_amd/csrc/paged_decode.hip", "nano-inference_amd/csrc/common.h")
+KV_WRITE_SOURCES = ("nano-inference_amd/csrc/kv_write.hip", "nano-inference_amd/csrc/common.h")
+
+
+def read_traffic(workload: str, sources=DECODE_SOURCES):
+    """Per-launch HBM bytes of a kernel from its committed counter summary
+    (profiles/traffic_<workload>.txt), or None when there is none or when it was measured
+    on other kernel sources (its source_sha256 line differs from the sources here)."""
     path = os.path.join(ROOT, "profiles", f"traffic_{workload}.txt")
     if not os.path.exists(path):
         return None
-    vals = {}
+    vals, digest = {}, None
     with open(path) as f:
         for line in f:
+            m = re.match(r"\s*source_sha256\s*[:=]\s*([0-9a-f]{64})", line)
+            if m:
+                digest = m.group(1)
+                continue
             m = re.match(r"\s*(\w+)\s*[:=]\s*([0-9.eE+-]+)", line)
             if m:
                 vals[m.group(1)] = float(m.group(2))
-    if "hbm_bytes_per_launch" in vals:
-        return vals["hbm_bytes_per_launch"]
-    return None
+    if digest != source_digest(sources):
+        return None
+    return vals.get("hbm_bytes_per_launch")
 
 
 def bench_decode(torch, ops, workloads, steps: int, warmup: int):
@@ -235,7 +256,8 @@ def bench_kv_write_prefill(torch, ops, workloads):
     byts = 4 * t * hk * d * c.k.element_size() + 8 * t
     return dict(us=round(ms * 1e3, 2), tokens=t, bytes=byts,
                 gbps=round(byts / (ms * 1e-3) / 1e9, 1),
-                frac=round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4))
+                frac=round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                traffic=read_traffic("kv_write_prefill_qwen3_8b", KV_WRITE_SOURCES))
 
 
 def bench_decode_vl(torch, ops, workloads):
@@ -251,7 +273,8 @@ def bench_decode_vl(torch, ops, workloads):
     ms = time_calls(torch, decode, 30)
     gbps = c.decode_bytes() / (ms * 1e-3) / 1e9
     return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
-                bytes=c.decode_bytes(), timing="median of 5 batches of 30 back-to-back calls")
+                bytes=c.decode_bytes(), traffic=read_traffic("decode_qwen25vl"),
+                timing="median of 5 batches of 30 back-to-back calls")
 
 
 def bench_decode_fp8(torch, ops, workloads, c):
@@ -271,7 +294,8 @@ def bench_decode_fp8(torch, ops, workloads, c):
     gbps = byts / (ms * 1e-3) / 1e9
     del f8
     return dict(ms=round(ms, 4), gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
-                bytes=byts, format="e4m3 codes + fp32 scale per (token, KV head) row",
+                bytes=byts, traffic=read_traffic("decode_fp8_qwen3_8b"),
+                format="e4m3 codes + fp32 scale per (token, KV head) row",
                 timing="median of 5 batches of 30 back-to-back calls")
 
 
@@ -312,72 +336,200 @@ def bench_e2e_eager(torch):
                 host_per_call=ht.per_call_us())
 
 
-def cpu_baseline(torch, workloads, budget_s: float = 20.0):
-    """The reference's decode attention (op-for-op CPU restatement), fp32, on a sample.
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    Sample: the first 8 sequences of the decode workload (same lengths, same
-    head layout), the reference's write loop + padded gather + repeat_interleave
-    + materialised softmax, repeated until about ``budget_s`` seconds have passed.
-    """
+
+def _median_ms(fn, runs: int, budget_s: float) -> float:
+    """One warm-up run, then the median of at least ``runs`` runs (more while the budget
+    lasts, at most 50)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < runs or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2] * 1e3
+
+
+def cpu_baseline(torch, workloads, budget_s: float = 20.0):
+    """The reference's attention, op for op on the host cores (the oracle's restatement of
+    layers/attention.py:12-50 and :267-332 and layers/vision.py:190-208), fp32, with the
+    KV write loop and the attention timed apart: config 1 in full, and the decode, causal
+    prefill and vision workloads on stated subsets (their padded fp32 scores would not
+    fit or would take minutes).  One warm-up run, then the median of >= 5 runs.  The
+    headline ``value`` is the decode subset's step (write + attention) in the units of
+    the GPU line."""
     from oracle import reference_attention as ref
+    from oracle import vision_windows as vw
 
     n = max(1, len(os.sched_getaffinity(0)))
     torch.set_num_threads(n)
-    lens = workloads.uniform_lengths(64, 512, 8192, 2002)[:8]
-    pool = sum(math.ceil(L / 16) for L in lens) + 64
-    c = workloads.make_decode(8, 32, 8, 128, lens, pool, 16, torch.float32, "cpu", 2002)
-    kc, vc = c.k_cache[0], c.v_cache[0]
-    mask = ref.decode_context_mask(c.context_lens)
+    each = budget_s / 5
 
-    def once():
-        ref.paged_attention(c.q.unsqueeze(1), c.k_new, c.v_new, kc, vc, c.slot_mapping,
-                            c.block_tables, c.context_lens, mask, is_prefill=False)
+    def decode_leg(c, runs):
+        kc, vc = c.k_cache[0], c.v_cache[0]
+        mask = ref.decode_context_mask(c.context_lens)
+        k4, v4 = c.k_new, c.v_new  # (B, 1, H_kv, D)
+        slots = c.slot_mapping  # (B, 1)
+        none = torch.full_like(slots, -1)  # attention alone: the loop finds no slot to write
+        w_ms = _median_ms(lambda: ref.kv_write_loop(k4, v4, kc, vc, slots), runs, each / 4)
+        a_ms = _median_ms(lambda: ref.paged_attention(c.q.unsqueeze(1), k4, v4, kc, vc, none,
+                                                      c.block_tables, c.context_lens, mask,
+                                                      is_prefill=False), runs, each)
+        byts_a, byts_w = c.decode_bytes(), c.write_bytes()
+        return dict(write_ms=round(w_ms, 3), attention_ms=round(a_ms, 3),
+                    attention_gbps=round(byts_a / (a_ms * 1e-3) / 1e9, 3),
+                    step_gbps=round((byts_a + byts_w) / ((a_ms + w_ms) * 1e-3) / 1e9, 3))
 
-    once()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        once()
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
-    times.sort()
-    med = times[len(times) // 2]
-    byts = c.decode_bytes() + c.write_bytes()
-    return dict(value=round(byts / med / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(),
-                kind="port",
-                sample=(f"reference decode attention (write loop, padded gather, "
-                        f"repeat_interleave, fp32 softmax) on the first 8 sequences of the "
-                        f"workload (contexts {lens}), fp32, median of {len(times)} runs, "
-                        f"{med * 1e3:.1f} ms per run; bytes counted at fp32 element size"))
+    legs = {}
+    c1 = workloads.decode_small("cpu", torch.float32, 1001)
+    legs["config1_decode_full"] = dict(
+        decode_leg(c1, 9), what="config 1 in full: batch 4, 16/8 heads, D 128, contexts "
+                                f"{c1.lens}, block 16")
+    lens2 = workloads.uniform_lengths(64, 512, 8192, 2002)[:8]
+    pool = sum(math.ceil(L / 16) for L in lens2) + 64
+    c2 = workloads.make_decode(8, 32, 8, 128, lens2, pool, 16, torch.float32, "cpu", 2002)
+    legs["config2_decode_subset"] = dict(
+        decode_leg(c2, 5), what=f"config 2, its first 8 sequences (contexts {lens2}), 32/8 "
+                                "heads, D 128")
+    # causal prefill: the shortest of config 3's sequences, through the reference's prefill
+    # branch (write loop over the step's tokens, repeat_interleave, causal sdpa)
+    lens3 = workloads.uniform_lengths(8, 256, 4096, 3003)
+    L3 = min(lens3)
+    c3 = workloads.make_varlen([L3], 32, 8, 128, torch.float32, "cpu", 3003, True)
+    q3, k3, v3 = (t.unsqueeze(0) for t in (c3.q, c3.k, c3.v))
+    nb3 = math.ceil(L3 / 16) + 1
+    kc3 = torch.zeros(nb3, 8, 16, 128)
+    vc3 = torch.zeros_like(kc3)
+    slots3 = torch.arange(L3, dtype=torch.int64).view(1, L3)
+    none3 = torch.full_like(slots3, -1)
+    w3 = _median_ms(lambda: ref.kv_write_loop(k3, v3, kc3, vc3, slots3), 5, each / 4)
+    a3 = _median_ms(lambda: ref.paged_attention(q3, k3, v3, kc3, vc3, none3, None, None, None,
+                                                is_prefill=True), 5, each)
+    legs["config3_prefill_subset"] = dict(
+        write_ms=round(w3, 3), attention_ms=round(a3, 3),
+        attention_gflops=round(c3.flops() / (a3 * 1e-3) / 1e9, 2),
+        what=f"config 3, its shortest sequence ({L3} tokens of {lens3}), causal, 32/8 heads")
+    # vision: the first image (28 x 28 patches), full attention and its 64-token windows
+    grid = [workloads.VISION_GRIDS[0]]
+    cu_full = vw.full_cu_seqlens(grid)
+    cu_win = vw.get_window_index(grid)[1]
+    S5 = int(cu_full[-1])
+    c5 = workloads.make_varlen([S5], 16, 16, 80, torch.float32, "cpu", 5105, False)
+    fl_full = 4 * 16 * 80 * S5 * S5
+    wl = [int(b - a) for a, b in zip(cu_win[:-1], cu_win[1:])]
+    fl_win = 4 * 16 * 80 * sum(x * x for x in wl)
+    af = _median_ms(lambda: ref.vision_attention(c5.q, c5.k, c5.v, cu_full), 5, each / 2)
+    aw = _median_ms(lambda: ref.vision_attention(c5.q, c5.k, c5.v, cu_win), 5, each / 2)
+    legs["config5_vision_subset"] = dict(
+        full_ms=round(af, 3), full_gflops=round(fl_full / (af * 1e-3) / 1e9, 2),
+        window_ms=round(aw, 3), window_gflops=round(fl_win / (aw * 1e-3) / 1e9, 2),
+        what=f"config 5, its first image ({grid[0][1]}x{grid[0][2]} patches, {S5} tokens), "
+             f"16 heads, D 80: full attention and its {len(wl)} windows")
+    lensv = workloads.uniform_lengths(32, 1024, 6144, 5005)[:4]
+    poolv = sum(math.ceil(L / 16) for L in lensv) + 64
+    cv = workloads.make_decode(4, 28, 4, 128, lensv, poolv, 16, torch.float32, "cpu", 5005)
+    legs["config5_decode_subset"] = dict(
+        decode_leg(cv, 5), what=f"config 5 language decode, its first 4 sequences (contexts "
+                                f"{lensv}), 28/4 heads, D 128")
+    head = legs["config2_decode_subset"]
+    return dict(value=head["step_gbps"], unit="GB/s", cores=torch.get_num_threads(),
+                kind="port", cpu_model=_cpu_model(), threads=torch.get_num_threads(),
+                sample=("reference decode step (per-token KV write loop + padded gather, "
+                        "repeat_interleave, fp32 softmax) on config 2's first 8 sequences, fp32; "
+                        "bytes counted at fp32 element size; the other legs as listed"),
+                legs=legs)
 
 
-def profile_decode(torch, ops, workloads, n: int) -> None:
-    """Minimal run for counter collection: a 1 GiB copy (calibration) and n decodes."""
+PROFILE_WORKLOADS = ("decode", "decode_vl", "decode_fp8", "kv_write", "kv_write_prefill",
+                     "prefill", "chunked", "vision_full", "vision_window")
+
+
+def profile_run(torch, ops, workloads, name: str, n: int) -> None:
+    """Minimal run for counter collection (rocprofv3 --pmc): three 1 GiB copies (the
+    calibration of FETCH_SIZE / WRITE_SIZE against known bytes), then n launches of one
+    workload's kernel(s) on the same inputs as the timed legs."""
     src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    c = workloads.decode_qwen3_8b("cuda", layers=DECODE_LAYERS)
-    for i in range(n):
-        L = i % DECODE_LAYERS
-        ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens)
+    del src, dst
+    info = {}
+    if name in ("decode", "decode_fp8", "kv_write"):
+        c = workloads.decode_qwen3_8b("cuda", layers=DECODE_LAYERS)
+        if name == "decode":
+            for i in range(n):
+                L = i % DECODE_LAYERS
+                ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens)
+            info = dict(algorithmic_bytes=c.decode_bytes())
+        elif name == "decode_fp8":
+            f8 = workloads.quantize_cache_fp8(c)
+            torch.cuda.synchronize()
+            for i in range(n):
+                L = i % DECODE_LAYERS
+                ops.paged_decode(c.q, f8.k_cache[L], f8.v_cache[L], c.block_tables,
+                                 c.context_lens, k_scale=f8.k_scale[L], v_scale=f8.v_scale[L])
+            info = dict(algorithmic_bytes=workloads.fp8_decode_bytes(c))
+        else:
+            for i in range(n):
+                L = i % DECODE_LAYERS
+                ops.kv_write(c.k_new, c.v_new, c.k_cache[L], c.v_cache[L], c.slot_mapping)
+            info = dict(algorithmic_bytes=c.write_bytes())
+    elif name == "decode_vl":
+        c = workloads.decode_vl("cuda", layers=DECODE_LAYERS)
+        for i in range(n):
+            L = i % DECODE_LAYERS
+            ops.paged_decode(c.q, c.k_cache[L], c.v_cache[L], c.block_tables, c.context_lens)
+        info = dict(algorithmic_bytes=c.decode_bytes())
+    elif name == "kv_write_prefill":
+        c = workloads.prefill_qwen3_8b("cuda")
+        t, hk, d = c.k.shape
+        bs = 16
+        nblk = 2 * ((t + bs - 1) // bs)
+        g = torch.Generator(device="cpu").manual_seed(7)
+        blocks = torch.randperm(nblk, generator=g)[: (t + bs - 1) // bs]
+        pos = torch.arange(t)
+        slots = (blocks[pos // bs] * bs + pos % bs).to(torch.int64).cuda()
+        kc = torch.zeros(nblk, hk, bs, d, dtype=c.k.dtype, device="cuda")
+        vc = torch.zeros_like(kc)
+        for _ in range(n):
+            ops.kv_write(c.k, c.v, kc, vc, slots)
+        info = dict(algorithmic_bytes=4 * t * hk * d * c.k.element_size() + 8 * t)
+    elif name == "chunked":
+        ch = workloads.chunked_qwen3_8b("cuda")
+        outc = torch.empty_like(ch.q)
+        for _ in range(n):
+            ops.prefill_paged(ch.q, ch.k_cache, ch.v_cache, ch.block_tables, ch.q_start,
+                              ch.q_len, ch.context_lens, ch.chunk, out=outc)
+        info = dict(flops=ch.flops())
+    elif name in ("prefill", "vision_full", "vision_window"):
+        if name == "prefill":
+            c = workloads.prefill_qwen3_8b("cuda")
+            mode = ops.CAUSAL_TOP_LEFT
+        else:
+            c = workloads.vision_vl("cuda", window=name == "vision_window")
+            mode = ops.CAUSAL_NONE
+        cu = c.cu_seqlens
+        qs, ql = cu[:-1].contiguous(), (cu[1:] - cu[:-1]).contiguous()
+        out = torch.empty_like(c.q)
+        for _ in range(n):
+            ops.prefill(c.q, c.k, c.v, qs, ql, qs, ql, max(c.lens), mode, out=out)
+        info = dict(flops=c.flops(), algorithmic_bytes=4 * c.q.numel() * c.q.element_size())
+    else:
+        raise SystemExit(f"bench.py: unknown profile workload {name!r}; one of "
+                         f"{', '.join(PROFILE_WORKLOADS)}")
     torch.cuda.synchronize()
-    print(json.dumps(dict(copy_bytes=1 << 30, decode_bytes=c.decode_bytes(),
-                          kv_bytes=c.kv_bytes())), flush=True)
-
-
-def profile_prefill(torch, ops, workloads, n: int) -> None:
-    """Minimal run for counter collection: n causal prefill launches."""
-    c = workloads.prefill_qwen3_8b("cuda")
-    cu = c.cu_seqlens
-    qs, ql = cu[:-1].contiguous(), (cu[1:] - cu[:-1]).contiguous()
-    out = torch.empty_like(c.q)
-    for _ in range(n):
-        ops.prefill(c.q, c.k, c.v, qs, ql, qs, ql, max(c.lens), ops.CAUSAL_TOP_LEFT, out=out)
-    torch.cuda.synchronize()
-    print(json.dumps(dict(flops=c.flops())), flush=True)
+    print(json.dumps(dict(workload=name, launches=n, copy_bytes=1 << 30, **info)), flush=True)
 
 
 def main() -> int:
@@ -387,8 +539,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--profile-decode", type=int, default=0)
-    ap.add_argument("--profile-prefill", type=int, default=0)
+    ap.add_argument("--profile", choices=PROFILE_WORKLOADS, default=None,
+                    help="only run --launches launches of one workload (counter runs)")
+    ap.add_argument("--launches", type=int, default=8)
     ap.add_argument("--no-e2e", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -403,11 +556,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
-    if args.profile_decode:
-        profile_decode(torch, ops, workloads, args.profile_decode)
-        return 0
-    if args.profile_prefill:
-        profile_prefill(torch, ops, workloads, args.profile_prefill)
+    if args.profile:
+        profile_run(torch, ops, workloads, args.profile, args.launches)
         return 0
 
     c, ms_step, dec_ms, wr_ms = bench_decode(torch, ops, workloads, args.steps, args.warmup)
@@ -419,7 +569,9 @@ def main() -> int:
     extra.update(bench_prefill(torch, ops, workloads))
     pf = extra["prefill_qwen3_8b"]
     extra["kv_write_qwen3_8b"] = dict(us=round(wr_ms * 1e3, 2),
-                                      gbps=round(c.write_bytes() / (wr_ms * 1e-3) / 1e9, 1))
+                                      gbps=round(c.write_bytes() / (wr_ms * 1e-3) / 1e9, 1),
+                                      bytes=c.write_bytes(),
+                                      traffic=read_traffic("kv_write_qwen3_8b", KV_WRITE_SOURCES))
     extra["kv_write_prefill_qwen3_8b"] = bench_kv_write_prefill(torch, ops, workloads)
     if not args.no_e2e:
         extra["e2e_qwen3_0p6b"] = bench_e2e(torch, mixed=True)
