@@ -600,7 +600,7 @@ def main() -> int:
             "context_tokens": sum(c.lens), "step_bytes": step_bytes,
         },
         "roofline": {
-            "kernel": "paged decode (partial + combine)",
+            "kernel": "paged decode (decode_split_kernel + decode_split_combine_kernel)",
             "bound": "hbm",
             "achieved": round(dec_gbps, 1),
             "peak": HBM_PEAK_GBPS,
