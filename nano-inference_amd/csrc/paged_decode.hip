@@ -80,6 +80,7 @@ struct DecodeParams {
   int32_t wph;    // slices per KV head (4 / hg)
   int32_t nhg;    // head groups (num_kv_heads / hg)
   int32_t grid;   // workgroups
+  int32_t first_wgs;  // workgroups dispatched first on their CU
   int32_t* ws_pfx;  // [batch + 1] units before each sequence (one head group)
   float* sp_ml;     // [grid * wph][2][hg][G] (m, l) of the partial of a range's first / last sequence
   float* sp_o;      // [grid * wph][2][hg][G][D]
@@ -524,6 +525,53 @@ constexpr int kSplitLdsBatch = 1024;   // batches whose unit prefix (and context
                                        // workgroup builds in LDS
 constexpr int kSplitMaxGrid = 512;     // workgroups at most (sizes the partial slots)
 
+// Range weights.  With two workgroups per CU the one dispatched second on its CU (ids
+// grid / 2 and up: the dispatcher fills every CU once before doubling up) streams ~10%
+// slower while both run (measured per workgroup over the Qwen3-8B decode: 0.77 vs 0.85
+// units/us, the same whichever ranges they get), so over bf16 caches the first ones take
+// kRangeFirst / kRangeSecond times as many units and both halves end together (decode
+// kernel 192 -> 187 us).  Over the fp8 format the halves are even (weighting them cost
+// 1.6 us), so its ranges stay equal.  Compile-time constants: read from the parameters,
+// the weights cost the split kernel ~20 scalar-register spills in its loop.
+template <bool FP8>
+struct RangeWeights {
+  static constexpr int kFirst = FP8 ? 1 : 6;
+  static constexpr int kSecond = FP8 ? 1 : 5;
+};
+
+// The ranges: virtual wave v starts at unit floor(total * W(v) / W(V)), where W sums the
+// weights of the virtual waves before v (the first `first` of them weigh WF, the others
+// WS).  The quotients are formed in fp64, where they are exact: the products stay below
+// 2^53 and a quotient that is not an integer lies at least 1 / W(V) >= 2^-16 from one, far
+// more than the rounding of a value below 2^31 (2^-22); an integer division of 64-bit
+// values would cost the combine ~0.8 us and the split kernel its spare scalar registers.
+template <bool FP8>
+struct RangeSplit {
+  static constexpr int64_t WF = RangeWeights<FP8>::kFirst, WS = RangeWeights<FP8>::kSecond;
+  int64_t total, first, nv, wt;
+  NIA_DEVICE RangeSplit(int64_t total_units, const DecodeParams& p)
+      : total(total_units),
+        first((int64_t)p.first_wgs * p.wph),
+        nv((int64_t)p.grid * p.wph),
+        wt(weight_before((int64_t)p.grid * p.wph, (int64_t)p.first_wgs * p.wph)) {}
+  static NIA_DEVICE int64_t weight_before(int64_t v, int64_t first) {
+    return v <= first ? WF * v : WF * first + WS * (v - first);
+  }
+  static NIA_DEVICE int64_t at(int64_t total, int64_t w, int64_t wt) {
+    return (int64_t)((double)total * (double)w / (double)wt);
+  }
+  NIA_DEVICE int64_t weight_before(int64_t v) const { return weight_before(v, first); }
+  NIA_DEVICE int64_t at(int64_t w) const { return at(total, w, wt); }
+  NIA_DEVICE int64_t start(int64_t v) const { return at(weight_before(v)); }
+  // the range holding unit u: the last v with start(v) <= u
+  NIA_DEVICE int64_t holding(int64_t u) const {
+    // the largest W(v) with start(v) <= u
+    const int64_t w = (int64_t)(((double)(u + 1) * (double)wt - 1.0) / (double)total);
+    const int64_t v = w < WF * first ? w / WF : first + (w - WF * first) / WS;
+    return v < nv - 1 ? v : nv - 1;
+  }
+};
+
 // 16-byte DMA global -> LDS with a wave-uniform byte offset (soffset) on top of the lane's.
 NIA_DEVICE void lds_dma16_s(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset,
                             uint8_t* lds_wave_base) {
@@ -574,8 +622,7 @@ NIA_DEVICE uint4 widen_fp8x8(uint32_t a, uint32_t b) {
 
 // One wave's position in the unit stream: unit u of head group g, pair j of sequence b.
 struct SplitUnit {
-  int64_t u;   // -1: past the wave's range
-  int64_t U0;  // first unit of (g, b)
+  int64_t u;  // -1: past the wave's range; the first unit of (g, b) is u - j
   int b, g, j, n, ctx;  // n: units of sequence b; ctx: its context length (clamped)
 };
 
@@ -605,15 +652,22 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
 
   // ---- units before each sequence (one head group), and the clamped context lengths -------
   const int* pfx = p.ws_pfx;  // large batches: written by decode_prefix_kernel
+  // the batch's unit prefix and context lengths in LDS (batch <= kSplitLdsBatch), or read
+  // from the workspace (decode_prefix_kernel) and context_lens
   const bool lds_index = batch <= kSplitLdsBatch;
   if (lds_index) {
     constexpr int kPer = kSplitLdsBatch / kDecodeThreads;
     const int b0 = tid * kPer;
     int units[kPer];
     int run = 0;
+    // the kPer loads go out together (indices clamped into the batch, which is not empty),
+    // and one wait covers them
+    int64_t cl[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) cl[k] = p.context_lens[min(b0 + k, batch - 1)];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      int64_t c = b0 + k < batch ? p.context_lens[b0 + k] : 0;
+      int64_t c = b0 + k < batch ? cl[k] : 0;
       c = c < 0 ? 0 : (c > cap ? cap : c);
       if (b0 + k < batch) s_ctx[b0 + k] = (int)c;
       units[k] = (int)((c + kUnitKeys - 1) / kUnitKeys);
@@ -637,35 +691,51 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   const int hg = p.hg, wph = p.wph;
   const int hig = wave % hg;   // KV head within the group
   const int slice = wave / hg;
-  const int64_t nv = (int64_t)p.grid * wph;
+  // the wave's range, [RangeSplit::start(vw), RangeSplit::start(vw + 1)), from the static
+  // pieces (a RangeSplit object here costs the loop ~25 scalar-register spills)
+  using Split = RangeSplit<FP8>;
   const int64_t vw = (int64_t)blockIdx.x * wph + slice;
-  const int64_t ustart = total * vw / nv;
-  const int64_t uend = total * (vw + 1) / nv;
+  const int64_t fv = (int64_t)p.first_wgs * wph;
+  const int64_t wt = Split::weight_before((int64_t)p.grid * wph, fv);
+  const int64_t ustart = Split::at(total, Split::weight_before(vw, fv), wt);
+  const int64_t uend = Split::at(total, Split::weight_before(vw + 1, fv), wt);
   if (ustart >= uend) return;  // no barrier follows: waves leave on their own
 
   // ---- walking the unit range ----------------------------------------------------------------
+  // The unit prefix and the context lengths come from LDS, or for large batches through
+  // scalar loads (the indices are wave-uniform): a flat or vector load here would also wait
+  // for the loads in flight.
+  using const_i32 = const __attribute__((address_space(4))) int32_t*;
+  using const_i64 = const __attribute__((address_space(4))) int64_t*;
   auto locate = [&](int64_t u, SplitUnit& x) __attribute__((always_inline)) {
     x.u = u;
     x.g = (int)(u / T);
     const int r = (int)(u - (int64_t)x.g * T);
     int lo = 0, hi = batch;  // pfx[lo] <= r < pfx[hi]; ends on the sequence holding r
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (pfx[mid] <= r) lo = mid; else hi = mid;
-    }
-    x.b = uniform(lo);
-    const int p0 = uniform(pfx[x.b]);
-    x.j = r - p0;
-    x.n = uniform(pfx[x.b + 1]) - p0;
-    x.U0 = (int64_t)x.g * T + p0;
-    int c;
+    int p0, p1, c;
     if (lds_index) {
-      c = s_ctx[x.b];
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (uniform(s_pfx[mid]) <= r) lo = mid; else hi = mid;
+      }
+      p0 = uniform(s_pfx[lo]);
+      p1 = uniform(s_pfx[lo + 1]);
+      c = uniform(s_ctx[lo]);
     } else {
-      const int64_t c64 = p.context_lens[x.b];
+      const const_i32 gp = (const_i32)p.ws_pfx;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (gp[mid] <= r) lo = mid; else hi = mid;
+      }
+      p0 = gp[lo];
+      p1 = gp[lo + 1];
+      const int64_t c64 = ((const_i64)p.context_lens)[lo];
       c = (int)(c64 < 0 ? 0 : (c64 > cap ? cap : c64));
     }
-    x.ctx = uniform(c);
+    x.b = lo;
+    x.j = r - p0;
+    x.n = p1 - p0;
+    x.ctx = c;
   };
   auto advance = [&](SplitUnit& x) __attribute__((always_inline)) {
     if (x.u < 0) return;
@@ -797,7 +867,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     float ls = l_run + __shfl_xor(l_run, 16, kWave);
     ls += __shfl_xor(ls, 32, kWave);
     const int hk = x.g * hg + hig;
-    const bool whole = x.U0 >= ustart && x.U0 + x.n <= uend;
+    const int64_t U0 = x.u - x.j;
+    const bool whole = U0 >= ustart && U0 + x.n <= uend;
     if (hn < G) {
       if (whole) {
         bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)x.b * p.out_b +
@@ -809,7 +880,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
               make_uint2(pack_bf16x2(oacc[mt][0] * inv, oacc[mt][1] * inv),
                          pack_bf16x2(oacc[mt][2] * inv, oacc[mt][3] * inv));
       } else {
-        const int sl = x.U0 <= ustart ? 0 : 1;
+        const int sl = U0 <= ustart ? 0 : 1;
         const int64_t row = ((vw * 2 + sl) * hg + hig) * G + hn;
         float* po = p.sp_o + row * D + 4 * quad;
 #pragma unroll
@@ -829,10 +900,15 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   advance(n2);
   int ids_c = load_ids(cur);
   int ids_1 = load_ids(n1);
+  // The first unit's table entries are needed at once.  Wait for them here, on every path:
+  // left to the compiler, the wait lands inside issue()'s per-tile branches, where it also
+  // covers the DMA of the tile before, and the first unit's tiles go out one round trip
+  // apart (about 6 us at launch).
+  __builtin_amdgcn_s_waitcnt(0);
+  issue(cur, ids_c, cur.g * hg + hig);
   uint4 qb[4];
   uint2 qt = make_uint2(0, 0);
   load_q(cur, qb, qt);
-  issue(cur, ids_c, cur.g * hg + hig);
   for (;;) {
     __builtin_amdgcn_s_waitcnt(0);  // this unit's tiles are in the slot
     uint4 ka[2][4];
@@ -877,7 +953,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
         va[t][mt] = lds_read_tr16(slot + 8192 * t + 4096 + off.v_read[mt]);
     __builtin_amdgcn_s_waitcnt(0);  // read out before the slot is refilled
     __builtin_amdgcn_sched_barrier(0);
-    const bool new_seg = n1.u < 0 || n1.U0 != cur.U0;
+    const bool new_seg = n1.u < 0 || n1.j == 0;  // units of a sequence follow each other
     if (n1.u >= 0) issue(n1, ids_1, n1.g * hg + hig);
     const int ids_2 = load_ids(n2);
     __builtin_amdgcn_sched_barrier(0);
@@ -1019,7 +1095,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_prefix_kernel(DecodePar
 // empty sequences get zeros; pairs finished by the split kernel are left alone.
 constexpr int kCombineRows = 16;
 
-template <int D>
+template <int D, bool FP8>
 __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(DecodeParams p,
                                                                                int batch) {
   static_assert(D <= 2 * kWave, "two output dims per lane");
@@ -1042,17 +1118,18 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
     return;
   }
   const int64_t total = (int64_t)T * p.nhg;
-  const int64_t nv = (int64_t)p.grid * p.wph;
+  const RangeSplit<FP8> split(total, p);
   const int64_t U0 = (int64_t)g * T + pb, U1 = U0 + n_units;
-  // the range holding unit u is the last vw with total * vw / nv <= u
-  const int64_t f = ((U0 + 1) * nv - 1) / total, e = (U1 * nv - 1) / total;
+  const int64_t f = split.holding(U0), e = split.holding(U1 - 1);
   if (f == e) return;  // one wave had the whole sequence and wrote it
   const int n = (int)(e - f + 1);
-  // range starts s(v) = floor(total * v / nv), stepped without divisions:
-  // s(v + 1) = s(v) + q + (carry of r over nv)
-  const int64_t q = total / nv, r = total - q * nv;
-  int64_t s_next = total * f / nv;
-  int64_t rem = total * f - s_next * nv;  // (total * v) mod nv
+  // range starts s(v) = floor(total * W(v) / wt), stepped without divisions: W grows by
+  // the range's weight w, so s grows by q_w plus the carry of r_w over wt
+  const int64_t wt = split.wt;
+  const int64_t qa = split.at(split.WF), ra = total * split.WF - qa * wt;
+  const int64_t qb = split.at(split.WS), rb = total * split.WS - qb * wt;
+  int64_t s_next = split.start(f);
+  int64_t rem = total * split.weight_before(f) - s_next * wt;  // (total * W(v)) mod wt
   float m_run = -INFINITY, l_run = 0.f;
   float2 acc = make_float2(0.f, 0.f);
   for (int c0 = 0; c0 < n; c0 += kCombineRows) {
@@ -1064,9 +1141,10 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
       const int64_t v = f + c0 + i;
       if (c0 + i < n) {
         const int64_t s0 = s_next;
-        rem += r;
-        s_next += q + (rem >= nv ? 1 : 0);
-        rem -= rem >= nv ? nv : 0;
+        const bool first = v < split.first;
+        rem += first ? ra : rb;
+        s_next += (first ? qa : qb) + (rem >= wt ? 1 : 0);
+        rem -= rem >= wt ? wt : 0;
         const int64_t s1 = s_next;
         if (s0 < s1) {  // an empty range wrote nothing
           const int sl = U0 <= s0 ? 0 : 1;
@@ -1136,17 +1214,21 @@ bool f32_partition_shape(int32_t head_dim, int32_t block_size, int32_t group) {
 }
 
 // Workgroups of the split kernel: as many as the chip holds at once (two per CU, 8 waves),
-// cached per (device, kernel).
+// and how many of them are dispatched first on their CU (one per CU), cached per
+// (device, kernel).
 std::mutex g_occ_mutex;
-std::map<std::pair<int, int>, int> g_occ;
+std::map<std::pair<int, int>, std::pair<int, int>> g_occ;
 
 template <int D, bool FP8>
-int split_grid(int device) {
+int split_grid(int device, int& first) {
   const int key = 2 * D + (FP8 ? 1 : 0);
   {
     std::lock_guard<std::mutex> lock(g_occ_mutex);
     auto it = g_occ.find({device, key});
-    if (it != g_occ.end()) return it->second;
+    if (it != g_occ.end()) {
+      first = it->second.second;
+      return it->second.first;
+    }
   }
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
@@ -1157,8 +1239,9 @@ int split_grid(int device) {
   per_cu = per_cu < 1 ? 1 : (per_cu > 2 ? 2 : per_cu);
   int grid = cus * per_cu;
   grid = grid < 1 ? 1 : (grid > kSplitMaxGrid ? kSplitMaxGrid : grid);
+  first = grid < cus ? grid : cus;
   std::lock_guard<std::mutex> lock(g_occ_mutex);
-  g_occ[{device, key}] = grid;
+  g_occ[{device, key}] = {grid, first};
   return grid;
 }
 
@@ -1166,16 +1249,18 @@ template <int D, bool FP8>
 int launch_split(DecodeParams& p, int batch, hipStream_t s) {
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return NIA_ERR_LAUNCH;
-  const int grid = split_grid<D, FP8>(device);
+  int first = 0;
+  const int grid = split_grid<D, FP8>(device, first);
   if (grid < 1) return NIA_ERR_LAUNCH;
   p.grid = grid;
+  p.first_wgs = first;
   if (batch > kSplitLdsBatch)
     hipLaunchKernelGGL(decode_prefix_kernel, dim3(1), dim3(kDecodeThreads), 0, s, p, batch);
   hipLaunchKernelGGL((decode_split_kernel<D, FP8>), dim3(grid), dim3(kDecodeThreads), 0, s, p,
                      batch);
   constexpr int kPairsPerGroup = kCombineThreads / kWave;
   const int64_t pairs = (int64_t)batch * p.num_heads;
-  hipLaunchKernelGGL((decode_split_combine_kernel<D>),
+  hipLaunchKernelGGL((decode_split_combine_kernel<D, FP8>),
                      dim3((unsigned)((pairs + kPairsPerGroup - 1) / kPairsPerGroup)),
                      dim3(kCombineThreads), 0, s, p, batch);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
@@ -1332,7 +1417,17 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
     return launch_f32_partitions(p, G, batch, s);
   }
 
-  // bf16 queries over bf16 caches or the fp8 format: the split kernel
+  // bf16 queries over bf16 caches or the fp8 format: the split kernel.  Its unit counts
+  // (32 keys of one head group) are bounded by the table width: a head group's units must
+  // fit an int (the prefix sums), and all of them 2^36 (the fp64 range arithmetic); a batch
+  // beyond that would stream more than 2^41 keys per head group.
+  {
+    const int64_t per_seq = (((int64_t)max_blocks_per_seq * block_size) + kUnitKeys - 1) / kUnitKeys;
+    const int64_t hgs = num_kv_heads % 4 == 0 ? 4 : (num_kv_heads % 2 == 0 ? 2 : 1);
+    const int64_t units = per_seq * batch;
+    if (units > INT32_MAX || units * (num_kv_heads / hgs) >= (int64_t)1 << 36)
+      return NIA_ERR_UNSUPPORTED;
+  }
   if ((uintptr_t)q % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 ||
       q_batch_stride % 8 || q_head_stride % 8 || (uintptr_t)out % 8 || out_batch_stride % 4 ||
       out_head_stride % 4)

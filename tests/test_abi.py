@@ -59,6 +59,11 @@ def test_validation_returns_codes_without_launching():
                                 p, 1 << 30, 0, None) == _lib.ERR_UNSUPPORTED
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 32, 1, 128, 16, 10, 0.1,
                                 p, 1 << 30, 0, None) == _lib.ERR_UNSUPPORTED
+    # decode: 2^16 sequences over a table 2^24 keys wide: 2^35 units of 32 keys, beyond the
+    # split kernel's int prefix sums
+    ws = ctypes.c_void_p(4096)
+    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 1 << 20, 1 << 20, p, 1 << 16, 32, 8,
+                                128, 16, 10, 0.1, ws, 1 << 40, 0, None) == _lib.ERR_UNSUPPORTED
     # decode: workspace too small for 2 partitions
     assert lib.nia_paged_decode(p, 128, 128, p, 1024, 128, p, p, p, 64, 64, p, 2, 8, 4, 128, 16,
                                 100, 0.1, None, 0, 0, None) == _lib.ERR_WORKSPACE
