@@ -176,10 +176,14 @@ def bench_decode(torch, ops, workloads, steps: int, warmup: int):
     e.record()
     torch.cuda.synchronize()
     ms_step = a.elapsed_time(e) / steps
-    iters = max(steps, 20)
-    dec_ms = per_call_ms(torch, decode, iters)
+    iters = max(steps, 30)
+    # the launch duration: back-to-back calls between two events (what a kernel trace
+    # shows per launch); each call between events of its own also counts the event
+    # packets' dispatch latency (~5 us), reported beside it
+    dec_ms = time_calls(torch, decode, iters)
+    dec_bracketed_ms = per_call_ms(torch, decode, iters)
     wr_ms = graph_call_ms(torch, lambda _: write(0))
-    return c, ms_step, dec_ms, wr_ms
+    return c, ms_step, dec_ms, dec_bracketed_ms, wr_ms
 
 
 def bench_prefill(torch, ops, workloads):
@@ -560,7 +564,8 @@ def main() -> int:
         profile_run(torch, ops, workloads, args.profile, args.launches)
         return 0
 
-    c, ms_step, dec_ms, wr_ms = bench_decode(torch, ops, workloads, args.steps, args.warmup)
+    c, ms_step, dec_ms, dec_bracketed_ms, wr_ms = bench_decode(torch, ops, workloads, args.steps,
+                                                               args.warmup)
     step_bytes = c.decode_bytes() + c.write_bytes()
     value = step_bytes / (ms_step * 1e-3) / 1e9
     dec_gbps = c.decode_bytes() / (dec_ms * 1e-3) / 1e9
@@ -609,6 +614,8 @@ def main() -> int:
             "traffic": read_traffic("decode_qwen3_8b"),
             "algorithmic_bytes": c.decode_bytes(),
             "us_per_launch": round(dec_ms * 1e3, 2),
+            "timing": "back-to-back launches between two events, median of 5 rounds",
+            "us_per_launch_own_events": round(dec_bracketed_ms * 1e3, 2),
         },
         "prefill": {
             "workload": "causal varlen prefill, Qwen3-8B layout, 8 seqs U[256,4096]",

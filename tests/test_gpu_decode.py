@@ -206,3 +206,61 @@ def test_four_dim_query_and_explicit_scale():
     torch.cuda.synchronize()
     assert out4.shape == (4, 1, 16, 128)
     assert_attn_close(out4[:, 0], oracle_decode(c, scale=0.05), torch.float32, "scale 0.05")
+
+
+def test_one_workspace_shared_by_every_path_and_a_graph():
+    """One workspace shared by bf16 calls of several batch sizes (the LDS-indexed and the
+    large-batch prologue), an fp32 call (whose partitions overwrite the partial region)
+    and an fp8 call: every result equals the one computed with the cached workspace, and
+    repeated calls are bit-identical.  Then the same call captured in a HIP graph and
+    replayed three times, with eager calls on the same workspace in between."""
+    lens = [int(x) for x in torch.randint(1, 4097, (48,),
+                                          generator=torch.Generator().manual_seed(93))]
+    a = workloads.make_decode(48, 32, 8, 128, lens, 16384, 16, torch.bfloat16, "cuda",
+                              seed=93, max_blocks=256)
+    big = workloads.make_decode(1100, 16, 4, 128, [1 + i % 60 for i in range(1100)], 8192, 16,
+                                torch.bfloat16, "cuda", seed=94, max_blocks=4)
+    f32 = workloads.decode_small("cuda", torch.float32)
+    f8 = workloads.quantize_cache_fp8(a)
+    need = max(ops.decode_workspace_bytes(c.batch, c.q.shape[1], c.num_kv_heads,
+                                          c.block_tables.shape[1], 16, 128, c.q.dtype)
+               for c in (a, big, f32))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+
+    def call(c, workspace, fp8=False):
+        kw = dict(k_scale=f8.k_scale[0], v_scale=f8.v_scale[0]) if fp8 else {}
+        kc, vc = (f8.k_cache[0], f8.v_cache[0]) if fp8 else (c.k_cache[0], c.v_cache[0])
+        return ops.paged_decode(c.q, kc, vc, c.block_tables, c.context_lens,
+                                workspace=workspace, **kw)
+
+    expected = {}
+    for name, c, fp8 in (("a", a, False), ("big", big, False), ("f32", f32, False),
+                         ("fp8", a, True)):
+        expected[name] = call(c, None, fp8)
+    torch.cuda.synchronize()
+    for name, c, fp8 in (("a", a, False), ("f32", f32, False), ("big", big, False),
+                         ("fp8", a, True), ("a", a, False), ("a", a, False)):
+        out = call(c, ws, fp8)
+        torch.cuda.synchronize()
+        assert torch.equal(out, expected[name]), name
+    assert_attn_close(expected["a"], oracle_decode(a), torch.bfloat16, "shared workspace")
+
+    out = torch.empty_like(a.q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up off the capture
+        ops.paged_decode(a.q, a.k_cache[0], a.v_cache[0], a.block_tables, a.context_lens,
+                         out=out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.paged_decode(a.q, a.k_cache[0], a.v_cache[0], a.block_tables, a.context_lens,
+                         out=out, workspace=ws)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expected["a"])
+        assert torch.equal(call(big, ws), expected["big"])  # eager work in between
+        torch.cuda.synchronize()
