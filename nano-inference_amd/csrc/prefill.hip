@@ -489,7 +489,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2][kTileBytes];  // [stage][K, V]
+  // One array per stage and operand: the compiler then sees that the DMA into one stage
+  // cannot alias the LDS reads of the other and issues no vmcnt wait before those reads
+  // (with one [stage][K, V] array it waited for the next tile's DMA inside every tile).
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTileBytes];
+  auto tile_k = [&](int stage) __attribute__((always_inline)) { return stage ? lds_k1 : lds_k0; };
+  auto tile_v = [&](int stage) __attribute__((always_inline)) { return stage ? lds_v1 : lds_v0; };
 
   int seq, h, mb;
   if constexpr (PAIR) {
@@ -557,9 +565,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   const int bs_mask = (1 << p.bs_log2) - 1;
   // KV block holding this wave's 16-row group of tile n0 (first row clamped into the
   // context); -1 for an invalid id.
+  // A scalar load: a vector load here would be waited for with vmcnt(0), which also waits
+  // for the tile DMA just issued.
   auto block_of = [&](int n0) __attribute__((always_inline)) -> int {
     if constexpr (PAGED) {
-      const int b = bt[uniform(min(n0 + 16 * wave, klen - 1) >> p.bs_log2)];
+      using const_i32 = const __attribute__((address_space(4))) int32_t*;
+      const int b = ((const_i32)bt)[uniform(min(n0 + 16 * wave, klen - 1) >> p.bs_log2)];
       return (b < 0 || (int64_t)b >= p.num_blocks) ? -1 : b;
     } else {
       return 0;
@@ -623,8 +634,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     }
   };
   auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
-    issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, lds[stage][0], n0, blk, wave);
-    issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, lds[stage][1], n0, blk, wave);
+    issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, tile_k(stage), n0, blk, wave);
+    issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, tile_v(stage), n0, blk, wave);
   };
 
   // ---- per-lane LDS read offsets ---------------------------------------------------------
@@ -650,8 +661,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   }
 
   auto compute_tile = [&](int n0, int stage) __attribute__((always_inline)) {
-    const uint8_t* kt = lds[stage][0];
-    const uint8_t* vt = lds[stage][1];
+    const uint8_t* kt = tile_k(stage);
+    const uint8_t* vt = tile_v(stage);
     f32x16_t sacc[2];
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
@@ -760,15 +771,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       if (n0 > 0) __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, lds[hsel][0], n0, 0, 2 * wrow + g);
-        issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, lds[hsel][1], n0, 0, 2 * wrow + g);
+        issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, tile_k(hsel), n0, 0, 2 * wrow + g);
+        issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, tile_v(hsel), n0, 0, 2 * wrow + g);
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (n0 < wave_kend) compute_tile(n0, hsel);
     }
   } else if (n_end > 0) {
-  // ---- main loop: tile n0 in lds[stage] while tile n0 + 64 streams into the other --------
+  // ---- main loop: tile n0 in one stage while tile n0 + 64 streams into the other ---------
   // Unrolled by two so that each stage's LDS offsets are compile-time constants.
     int blk_nxt = block_of(0);
     issue_tile(0, 0, blk_nxt);
