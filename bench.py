@@ -121,6 +121,7 @@ def source_digest(paths) -> str:
 
 DECODE_SOURCES = ("nano-inference_amd/csrc/paged_decode.hip", "nano-inference_amd/csrc/common.h")
 KV_WRITE_SOURCES = ("nano-inference_amd/csrc/kv_write.hip", "nano-inference_amd/csrc/common.h")
+PREFILL_SOURCES = ("nano-inference_amd/csrc/prefill.hip", "nano-inference_amd/csrc/common.h")
 
 
 def read_traffic(workload: str, sources=DECODE_SOURCES):
@@ -232,7 +233,9 @@ def bench_prefill(torch, ops, workloads):
         if window:
             gbps = byts / (ms * 1e-3) / 1e9
             res[v.name + "_hbm"] = dict(gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4),
-                                        bytes=byts, bound="hbm")
+                                        bytes=byts, bound="hbm",
+                                        traffic=read_traffic("vision_window_qwen25vl",
+                                                             PREFILL_SOURCES))
         res[v.name] = dict(ms=round(ms, 4), tflops=round(tf, 1),
                            frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), chunks=len(v.lens),
                            flops=v.flops())
