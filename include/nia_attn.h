@@ -123,9 +123,8 @@ int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_s
  * replaced by a fixed array of NIA_DECODE_SCRATCH_BYTES in the library's device
  * memory (one per GPU, held until the process ends).  A call whose
  * nia_paged_decode_workspace_size(...) exceeds it returns NIA_ERR_SCRATCH_LIMIT before
- * anything is launched.  The first call on a device clears the array's header on
- * `stream`.  All calls on one GPU share the array: calls that overlap in time on one
- * GPU (other streams, other threads) race.
+ * anything is launched.  All calls on one GPU share the array: calls that overlap in
+ * time on one GPU (other streams, other threads) race.
  */
 #define NIA_DECODE_SCRATCH_BYTES (32u << 20)
 

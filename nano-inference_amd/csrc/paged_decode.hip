@@ -1180,7 +1180,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
 
 constexpr int kPartBlocks = 32;  // fp32 partition kernel: 512 tokens per partition
 
-// Workspace layout: [header (256 B)][per path:
+// Workspace layout: [header (256 B, reserved; nothing reads or writes it)][per path:
 //   split:  ws_pfx (batch + 1 ints, rounded to 256 B)][sp_ml][sp_o]
 //   fp32 partitions:  [ws_ml][ws_o]]
 constexpr size_t kHeaderBytes = 256;
@@ -1491,12 +1491,11 @@ extern "C" int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride,
 }
 
 // ---- decode without caller memory -------------------------------------------------------
-// The same kernels with their workspace (work counters, partition partials) in a fixed
-// device array of this library instead of caller memory, for callers that cannot
-// allocate (code under graph capture, serving loops that forbid allocation).  Every call
-// on a GPU shares that GPU's copy: the counters are cleared once, at the first call on
-// the device, and every completed call leaves them at zero again (as with a caller's
-// workspace); calls that overlap in time on one GPU race for the array.
+// The same kernels with their workspace (unit prefix, partials) in a fixed device array of
+// this library instead of caller memory, for callers that cannot allocate (code under graph
+// capture, serving loops that forbid allocation).  Nothing in a workspace is read before
+// the same call writes it, so the array needs no clearing; every call on a GPU shares that
+// GPU's copy, and calls that overlap in time on one GPU race for it.
 namespace {
 
 constexpr size_t kScratchBytes = (size_t)NIA_DECODE_SCRATCH_BYTES;
@@ -1507,23 +1506,16 @@ __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
-__global__ void scratch_clear_kernel(uint32_t* p, int words) {
-  for (int i = threadIdx.x; i < words; i += blockDim.x) p[i] = 0u;
-}
-
 std::mutex g_scratch_mutex;
 std::vector<void*> g_scratch_ptr;  // per device: the device address of `scratch`
 
-// The device address of this GPU's `scratch` (looked up, and its counters cleared on
-// `stream`, at the first call on the device), or null when the lookup fails.
-void* device_scratch(int device, hipStream_t stream) {
+// The device address of this GPU's `scratch` (looked up at the first call on the device),
+// or null when the lookup fails.
+void* device_scratch(int device) {
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if ((size_t)device < g_scratch_ptr.size() && g_scratch_ptr[device]) return g_scratch_ptr[device];
   void* ptr = nullptr;
   if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
-  hipLaunchKernelGGL(scratch_clear_kernel, dim3(1), dim3(64), 0, stream,
-                     reinterpret_cast<uint32_t*>(ptr), (int)(kHeaderBytes / 4));
-  if (hipGetLastError() != hipSuccess) return nullptr;
   if (g_scratch_ptr.size() <= (size_t)device) g_scratch_ptr.resize(device + 1, nullptr);
   g_scratch_ptr[device] = ptr;
   return ptr;
@@ -1551,7 +1543,7 @@ extern "C" int32_t nia_paged_decode_noalloc(void* out, int64_t out_batch_stride,
   if (need > kScratchBytes) return NIA_ERR_SCRATCH_LIMIT;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0) return NIA_ERR_LAUNCH;
-  void* ws = device_scratch(device, (hipStream_t)stream);
+  void* ws = device_scratch(device);
   if (!ws) return NIA_ERR_LAUNCH;
   return paged_decode_entry(out, out_batch_stride, out_head_stride, q, q_batch_stride,
                             q_head_stride, k_cache, v_cache, nullptr, nullptr, false,
