@@ -552,7 +552,7 @@ def main() -> int:
     ap.add_argument("--no-e2e", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+        print(f"bench.py: measures one GPU only (--gpus {args.gpus} requested); "
               "the attention path has no multi-GPU leg", file=sys.stderr)
         return 2
 

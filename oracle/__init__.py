@@ -1,6 +1,6 @@
 """Oracle for the nano-inference attention path - TEST INFRASTRUCTURE ONLY.
 
-This package is the checker, never the thing measured or shipped.  Only the
+This package checks the HIP path; it is never the thing measured or shipped.  Only the
 tests, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``
 may import it.  The product path (``nano_inference_amd``) never imports it and
 fails loudly when its HIP library is missing.
