@@ -3,6 +3,13 @@
 The library is built in-tree (``build_lib.py``) and loaded from the package
 directory.  There is no fallback: if the library is missing, every attention
 call raises, so a GPU run can never silently take another path.
+
+``calls()`` is what the per-layer ops call: the CPython fast-call module
+``_nia_fast`` bound to this same library (one library instance, one device
+state), which converts the ~23 integer arguments of a call in well under a
+microsecond where ctypes takes a few; the ctypes library itself where that
+module has not been built.  Both take the arguments of nia_attn.h in order and
+return the int status.
 """
 from __future__ import annotations
 
@@ -102,8 +109,22 @@ SIGNATURES = {
 
 ABI_VERSION = 2
 
+# The entry points _nia_fast wraps: one call per layer and step.
+FAST_CALLS = (
+    "nia_kv_write",
+    "nia_kv_write_fp8",
+    "nia_paged_decode",
+    "nia_paged_decode_fp8",
+    "nia_prefill",
+    "nia_prefill_paged",
+    "nia_qk_norm_rope_kv_write",
+    "nia_qk_norm_rope_kv_write_fp8",
+)
+
 _lock = threading.Lock()
 _lib: C.CDLL | None = None
+_calls = None
+_calls_lib: C.CDLL | None = None
 
 
 class NiaError(RuntimeError):
@@ -141,6 +162,32 @@ def load() -> C.CDLL:
                 raise ImportError(f"{path}: ABI version {got}, expected {ABI_VERSION}")
             _lib = lib
     return _lib
+
+
+def fast_module():
+    """The _nia_fast extension module, or None where it has not been built."""
+    try:
+        from . import _nia_fast
+    except ImportError:
+        return None
+    return _nia_fast
+
+
+def calls():
+    """The hot entry points (``FAST_CALLS``): _nia_fast bound to the loaded library, or
+    the ctypes library where _nia_fast is absent.  Loads the library like ``load()``."""
+    global _calls, _calls_lib
+    lib = load()
+    if _calls is not None and _calls_lib is lib:
+        return _calls
+    with _lock:
+        if _calls is None or _calls_lib is not lib:
+            fast = fast_module()
+            if fast is not None:
+                for name in FAST_CALLS:
+                    fast.bind(name, C.cast(getattr(lib, name), C.c_void_p).value)
+            _calls, _calls_lib = (fast if fast is not None else lib), lib
+    return _calls
 
 
 def check(fn: str, status: int) -> None:

@@ -3,7 +3,10 @@
 Usage: python build_lib.py [-v]   (from any directory)
 
 Every HIP source under csrc/ is compiled for gfx950 only and linked into one
-shared library next to this file.  Objects go to _build/ (git-ignored).
+shared library next to this file.  Objects go to _build/ (git-ignored).  The
+CPython fast-call module (csrc/fastcall.c, which calls that library's hot entry
+points through pointers handed to it at load time) is compiled with the host C
+compiler into the same directory.
 """
 from __future__ import annotations
 
@@ -12,12 +15,15 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_NAME = "libnia_attn.so"
+FAST_SRC = CSRC / "fastcall.c"
+FAST_NAME = "_nia_fast" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
@@ -81,6 +87,32 @@ def build(verbose: bool = False) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, out)
+    build_fast(verbose)
+    return out
+
+
+def build_fast(verbose: bool = False) -> Path | None:
+    """Compile the CPython fast-call module next to the library; returns its path.
+
+    Without a host C compiler or Python's headers it is skipped with a warning: the
+    ctypes binding then makes the same calls, at a few microseconds more per call.
+    """
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    inc = sysconfig.get_paths().get("include")
+    if not cc or not inc or not (Path(inc) / "Python.h").exists():
+        print(f"warning: {FAST_NAME} not built (no C compiler or Python.h); "
+              "the hot calls go through ctypes", file=sys.stderr)
+        return None
+    out = PKG_DIR / FAST_NAME
+    tmp = PKG_DIR / (FAST_NAME + ".tmp")
+    cmd = [cc, "-O2", "-Wall", "-Wextra", "-Werror", "-shared", "-fPIC", f"-I{inc}",
+           str(FAST_SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{FAST_SRC.name} failed to compile:\n{res.stderr}")
     os.replace(tmp, out)
     return out
 

@@ -20,6 +20,24 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 #define NIA_DEVICE __device__ __forceinline__
 
+// ---- launches (host) ------------------------------------------------------------
+
+template <typename T>
+struct NiaArg {
+  using type = T;
+};
+
+// Launch `kernel` with hipLaunchKernel and its arguments' addresses: the launch the <<< >>>
+// form makes, without its push and pop of a call configuration (about 0.5 us of host time
+// per launch).  The arguments convert to the kernel's parameter types as in a call; a
+// failure is left in hipGetLastError(), as with <<< >>>.
+template <typename... A>
+inline void nia_launch(void (*kernel)(A...), dim3 grid, dim3 block, hipStream_t stream,
+                       typename NiaArg<A>::type... args) {
+  void* ptrs[] = {(void*)&args...};
+  (void)hipLaunchKernel((const void*)kernel, grid, block, ptrs, 0, stream);
+}
+
 constexpr int kWave = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 

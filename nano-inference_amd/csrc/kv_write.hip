@@ -86,10 +86,10 @@ extern "C" int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_h
     const int64_t work = rows * (row_bytes / vec);
     const int64_t blocks = (work + 255) / 256;
     const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, s, (const uint8_t*)k, kt, kh,
-                       (const uint8_t*)v, vt, vh, (uint8_t*)k_cache, (uint8_t*)v_cache,
-                       slot_mapping, num_tokens, num_kv_heads, (int32_t)row_bytes, block_size,
-                       num_slots);
+    nia_launch(kernel, dim3(grid), dim3(256), s, (const uint8_t*)k, kt, kh,
+               (const uint8_t*)v, vt, vh, (uint8_t*)k_cache, (uint8_t*)v_cache,
+               slot_mapping, num_tokens, num_kv_heads, (int32_t)row_bytes, block_size,
+               num_slots);
   };
   if (fits(16))
     launch(kv_write_kernel<16>, 16);
@@ -172,17 +172,15 @@ extern "C" int32_t nia_kv_write_fp8(const void* k, int64_t k_tok_stride, int64_t
   const int64_t num_slots = num_blocks * block_size;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NIA_DTYPE_BF16)
-    hipLaunchKernelGGL(kv_write_fp8_kernel<bf16_t>, dim3((unsigned)groups), dim3(kFp8Rows * kWave),
-                       0, s, (const bf16_t*)k, k_tok_stride, k_head_stride, (const bf16_t*)v,
-                       v_tok_stride, v_head_stride, (uint8_t*)k_cache, (uint8_t*)v_cache,
-                       k_scale, v_scale, slot_mapping, num_tokens, num_kv_heads, block_size,
-                       num_slots);
+    nia_launch(kv_write_fp8_kernel<bf16_t>, dim3((unsigned)groups), dim3(kFp8Rows * kWave), s,
+               (const bf16_t*)k, k_tok_stride, k_head_stride, (const bf16_t*)v, v_tok_stride,
+               v_head_stride, (uint8_t*)k_cache, (uint8_t*)v_cache, k_scale, v_scale,
+               slot_mapping, num_tokens, num_kv_heads, block_size, num_slots);
   else
-    hipLaunchKernelGGL(kv_write_fp8_kernel<float>, dim3((unsigned)groups), dim3(kFp8Rows * kWave),
-                       0, s, (const float*)k, k_tok_stride, k_head_stride, (const float*)v,
-                       v_tok_stride, v_head_stride, (uint8_t*)k_cache, (uint8_t*)v_cache,
-                       k_scale, v_scale, slot_mapping, num_tokens, num_kv_heads, block_size,
-                       num_slots);
+    nia_launch(kv_write_fp8_kernel<float>, dim3((unsigned)groups), dim3(kFp8Rows * kWave), s,
+               (const float*)k, k_tok_stride, k_head_stride, (const float*)v, v_tok_stride,
+               v_head_stride, (uint8_t*)k_cache, (uint8_t*)v_cache, k_scale, v_scale,
+               slot_mapping, num_tokens, num_kv_heads, block_size, num_slots);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
@@ -254,10 +252,10 @@ extern "C" int32_t nia_dequant_gather_fp8(const void* k_cache, const void* v_cac
   const int64_t rows = (int64_t)max_blocks_per_seq * block_size * 2 * num_kv_heads;
   const int64_t groups = (rows + kFp8Rows - 1) / kFp8Rows;
   if (groups >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(dequant_gather_fp8_kernel, dim3((unsigned)groups, (unsigned)batch),
-                     dim3(kFp8Rows * kWave), 0, (hipStream_t)stream, (const uint8_t*)k_cache,
-                     (const uint8_t*)v_cache, k_scale, v_scale, block_tables, bt_stride,
-                     max_blocks_per_seq, context_lens, num_kv_heads, block_size, num_blocks,
-                     (bf16_t*)out_k, (bf16_t*)out_v, seq_stride);
+  nia_launch(dequant_gather_fp8_kernel, dim3((unsigned)groups, (unsigned)batch),
+             dim3(kFp8Rows * kWave), (hipStream_t)stream, (const uint8_t*)k_cache,
+             (const uint8_t*)v_cache, k_scale, v_scale, block_tables, bt_stride,
+             max_blocks_per_seq, context_lens, num_kv_heads, block_size, num_blocks,
+             (bf16_t*)out_k, (bf16_t*)out_v, seq_stride);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }

@@ -1255,14 +1255,14 @@ int launch_split(DecodeParams& p, int batch, hipStream_t s) {
   p.grid = grid;
   p.first_wgs = first;
   if (batch > kSplitLdsBatch)
-    hipLaunchKernelGGL(decode_prefix_kernel, dim3(1), dim3(kDecodeThreads), 0, s, p, batch);
-  hipLaunchKernelGGL((decode_split_kernel<D, FP8>), dim3(grid), dim3(kDecodeThreads), 0, s, p,
-                     batch);
+    nia_launch(decode_prefix_kernel, dim3(1), dim3(kDecodeThreads), s, p, batch);
+  nia_launch((decode_split_kernel<D, FP8>), dim3(grid), dim3(kDecodeThreads), s, p,
+             batch);
   constexpr int kPairsPerGroup = kCombineThreads / kWave;
   const int64_t pairs = (int64_t)batch * p.num_heads;
-  hipLaunchKernelGGL((decode_split_combine_kernel<D, FP8>),
-                     dim3((unsigned)((pairs + kPairsPerGroup - 1) / kPairsPerGroup)),
-                     dim3(kCombineThreads), 0, s, p, batch);
+  nia_launch((decode_split_combine_kernel<D, FP8>),
+             dim3((unsigned)((pairs + kPairsPerGroup - 1) / kPairsPerGroup)),
+             dim3(kCombineThreads), s, p, batch);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
@@ -1271,8 +1271,8 @@ int launch_f32_partitions(const DecodeParams& p, int G, int batch, hipStream_t s
   switch (G) {
 #define NIA_CASE(GG)                                                                          \
   case GG:                                                                                    \
-    hipLaunchKernelGGL((paged_decode_partial_kernel<float, 128, GG, 16, kPartBlocks>), grid,  \
-                       dim3(kDecodeThreads), 0, s, p);                                        \
+    nia_launch((paged_decode_partial_kernel<float, 128, GG, 16, kPartBlocks>), grid,          \
+               dim3(kDecodeThreads), s, p);                                                   \
     break;
     NIA_CASE(1)
     NIA_CASE(2)
@@ -1289,9 +1289,9 @@ int launch_f32_partitions(const DecodeParams& p, int G, int batch, hipStream_t s
   if (p.max_parts > 1) {
     constexpr int kPairsPerGroup = kCombineThreads / kWave;
     const int pairs = batch * p.num_heads;
-    hipLaunchKernelGGL((paged_decode_combine_kernel<float, 128, 16, kPartBlocks>),
-                       dim3((pairs + kPairsPerGroup - 1) / kPairsPerGroup), dim3(kCombineThreads),
-                       0, s, p, batch);
+    nia_launch((paged_decode_combine_kernel<float, 128, 16, kPartBlocks>),
+               dim3((pairs + kPairsPerGroup - 1) / kPairsPerGroup), dim3(kCombineThreads), s, p,
+               batch);
   }
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }

@@ -836,9 +836,9 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
 #define NIA_PREFILL_CASE(DD)                                                                 \
   case DD:                                                                                   \
     if (dma_ok)                                                                              \
-      hipLaunchKernelGGL((prefill_dma_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), 0, s, p); \
+      nia_launch((prefill_dma_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), s, p);        \
     else                                                                                     \
-      hipLaunchKernelGGL((prefill_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), 0, s, p); \
+      nia_launch((prefill_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), s, p);            \
     break;
     NIA_PREFILL_CASE(64)
     NIA_PREFILL_CASE(80)
@@ -958,8 +958,8 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
     switch (head_dim) {
 #define NIA_PAIR_CASE(DD)                                                                       \
   case DD:                                                                                      \
-    hipLaunchKernelGGL((prefill_dma_kernel<DD, false, true>), dim3((unsigned)nwg),              \
-                       dim3(kPrefillThreads), 0, st, p);                                        \
+    nia_launch((prefill_dma_kernel<DD, false, true>), dim3((unsigned)nwg),                      \
+               dim3(kPrefillThreads), st, p);                                                   \
     break;
       NIA_PAIR_CASE(64)
       NIA_PAIR_CASE(80)

@@ -216,9 +216,9 @@ int32_t launch_prefill_f32(const PrefillF32Params& p, bool paged, int head_dim, 
 #define NIA_F32_CASE(DD)                                                                      \
   case DD:                                                                                    \
     if (paged)                                                                                \
-      hipLaunchKernelGGL((prefill_f32_kernel<DD, true>), grid, dim3(kF32Threads), 0, stream, p); \
+      nia_launch((prefill_f32_kernel<DD, true>), grid, dim3(kF32Threads), stream, p);         \
     else                                                                                      \
-      hipLaunchKernelGGL((prefill_f32_kernel<DD, false>), grid, dim3(kF32Threads), 0, stream, p); \
+      nia_launch((prefill_f32_kernel<DD, false>), grid, dim3(kF32Threads), stream, p);        \
     break;
     NIA_F32_CASE(64)
     NIA_F32_CASE(80)

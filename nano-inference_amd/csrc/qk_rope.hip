@@ -215,14 +215,14 @@ int32_t launch_qk_norm_rope(
   const dim3 grid((unsigned)groups), block(kRows * kWave);
   if (dtype == NIA_DTYPE_BF16) {
     if (fp8)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<bf16_t, true>), grid, block, 0, s, p);
+      nia_launch((qk_norm_rope_kernel<bf16_t, true>), grid, block, s, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<bf16_t, false>), grid, block, 0, s, p);
+      nia_launch((qk_norm_rope_kernel<bf16_t, false>), grid, block, s, p);
   } else {
     if (fp8)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<float, true>), grid, block, 0, s, p);
+      nia_launch((qk_norm_rope_kernel<float, true>), grid, block, s, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<float, false>), grid, block, 0, s, p);
+      nia_launch((qk_norm_rope_kernel<float, false>), grid, block, s, p);
   }
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }

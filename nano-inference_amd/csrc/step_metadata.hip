@@ -190,7 +190,7 @@ extern "C" int32_t nia_step_metadata(
   p.block_tables = block_tables;
   p.mrope = mrope;
   const dim3 grid((unsigned)((width + kMetaThreads - 1) / kMetaThreads), (unsigned)batch);
-  hipLaunchKernelGGL(step_metadata_kernel, grid, dim3(kMetaThreads), 0, (hipStream_t)stream, p);
+  nia_launch(step_metadata_kernel, grid, dim3(kMetaThreads), (hipStream_t)stream, p);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }
 
@@ -233,7 +233,7 @@ extern "C" int32_t nia_step_metadata_packed(
   p.q_len = q_len;
   p.block_tables = block_tables;
   const dim3 grid((unsigned)((width + kMetaThreads - 1) / kMetaThreads), (unsigned)batch);
-  hipLaunchKernelGGL(step_metadata_packed_kernel, grid, dim3(kMetaThreads), 0,
-                     (hipStream_t)stream, p);
+  nia_launch(step_metadata_packed_kernel, grid, dim3(kMetaThreads),
+             (hipStream_t)stream, p);
   return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
 }

@@ -53,29 +53,35 @@ def _last_contig(name: str, t: torch.Tensor) -> None:
 
 
 class TensorMemo:
-    """Results derived from a tensor by reading it back to the host, kept while the same
-    tensor object comes back unmodified (same version counter), so that the layers of a
-    step which share one attention mask or one cu_seqlens tensor synchronise with the
-    device once instead of once per layer.  Holds strong references to the last
-    ``size`` tensors (masks and cu_seqlens: small), so that a freed tensor's memory and
-    id cannot come back as a different tensor with a stale result."""
+    """Results derived from a tensor, kept while the same tensor object comes back
+    unmodified (same version counter): values read back to the host, so that the layers
+    of a step which share one attention mask or one cu_seqlens tensor synchronise with
+    the device once instead of once per layer, and converted copies, so that a table
+    every layer passes is converted once.  Holds strong references to the last ``size``
+    tensors put (small ones), so that a freed tensor's memory and id cannot come back as
+    a different tensor with a stale result.  Lookups are one dict probe, whatever the
+    size."""
 
     def __init__(self, size: int = 8):
         self.size = size
-        self._items: list = []
+        self._items: dict = {}  # (id(tensor), key) -> (tensor, version, value), oldest first
 
     def get(self, t: torch.Tensor, key):
-        for item in self._items:
-            if item[0] is t and item[1] == t._version and item[2] == key:
-                return item[3]
+        item = self._items.get((id(t), key))
+        if item is not None and item[0] is t and item[1] == t._version:
+            return item[2]
         return None
 
     def put(self, t: torch.Tensor, key, value) -> None:
-        self._items.insert(0, (t, t._version, key, value))
-        del self._items[self.size:]
+        k = (id(t), key)
+        self._items.pop(k, None)
+        self._items[k] = (t, t._version, value)
+        while len(self._items) > self.size:
+            del self._items[next(iter(self._items))]
 
 
 _MAX_SEQLEN = TensorMemo()
+_INV_FREQ_F32 = TensorMemo(size=512)  # one table per layer (64 floats each)
 
 
 def _default_scale(head_dim: int, scale: Optional[float]) -> float:
@@ -154,7 +160,7 @@ def kv_write(
     slots = slot_mapping.reshape(-1).contiguous()
     if slots.numel() != k2.shape[0]:
         raise ValueError(f"{slots.numel()} slots for {k2.shape[0]} tokens")
-    lib = _lib.load()
+    lib = _lib.calls()
     if fp8:
         st = lib.nia_kv_write_fp8(
             k2.data_ptr(), k2.stride(0), k2.stride(1),
@@ -255,7 +261,8 @@ class _DecodePlan:
     (shapes, strides, dtypes, devices), so that a repeated call only reads pointers."""
 
     __slots__ = ("squeeze", "b", "h", "d", "hkv", "bs", "nb", "max_blocks", "dt", "fp8",
-                 "scale", "need", "bt_copy", "ctx_copy", "out_shape", "out_dtype")
+                 "scale", "need", "bt_copy", "ctx_copy", "device",
+                 "q_st", "out_st", "bt_st")
 
 
 _DECODE_PLANS: dict = {}
@@ -313,7 +320,20 @@ def _decode_plan(q, k_cache, v_cache, block_tables, context_lens, scale, out, k_
     pl.need = decode_workspace_bytes(b, h, hkv, max_blocks, bs, d, q3.dtype)
     pl.bt_copy = block_tables.stride(1) != 1
     pl.ctx_copy = not context_lens.is_contiguous()
-    pl.out_shape, pl.out_dtype = (b, h, d), q3.dtype
+    pl.device = q.device
+    # strides of the (B, H, D) views the kernel reads and writes: q[:, 0] and out[:, 0]
+    # start at q's and out's first element, so a call passes their pointers directly.
+    # Without `out`, a call allocates empty_like(q) (q's shape, and its layout when q is
+    # dense), whose strides follow from q's: taken here from one such allocation.
+    pl.q_st = q3.stride()[:2]
+    if out is None:
+        like = torch.empty_like(q)
+        pl.out_st = (like.stride(0), like.stride(2 if squeeze else 1))
+        if like.stride(-1) != 1:
+            raise ValueError("q's layout gives an output without a contiguous last dimension")
+    else:
+        pl.out_st = out3.stride()[:2]
+    pl.bt_st = max_blocks if pl.bt_copy else block_tables.stride(0)
     return pl
 
 
@@ -343,7 +363,8 @@ def paged_decode(
     A call is validated in full the first time its arguments' shapes, strides, dtypes
     and devices are seen; later calls with the same signature reuse that result.
     """
-    sig = (q.shape, q.stride(), q.dtype, q.get_device(),
+    dq = q.get_device()
+    sig = (q.shape, q.stride(), q.dtype, dq,
            k_cache.shape, k_cache.stride(), k_cache.dtype, k_cache.get_device(),
            v_cache.shape, v_cache.stride(), v_cache.dtype, v_cache.get_device(),
            block_tables.shape, block_tables.stride(), block_tables.dtype,
@@ -362,34 +383,32 @@ def paged_decode(
         if len(_DECODE_PLANS) >= _PLAN_CACHE_MAX:
             _DECODE_PLANS.clear()
         _DECODE_PLANS[sig] = pl
-    q3 = q[:, 0] if pl.squeeze else q
-    dev_index = q.get_device()
-    stream = _raw_stream(dev_index)
+    stream = _raw_stream(dq)
     if workspace is None:
-        ws = _DECODE_WS.get((dev_index, stream))
+        ws = _DECODE_WS.get((dq, stream))
         if ws is None or ws.numel() < pl.need:
-            ws = decode_workspace(q.device, pl.need)
+            ws = decode_workspace(pl.device, pl.need)
+        ws_bytes = ws.numel()  # uint8
     else:
         ws = workspace
-        if ws.numel() * ws.element_size() < pl.need:
-            raise ValueError(f"decode workspace of {ws.numel() * ws.element_size()} bytes, "
-                             f"{pl.need} needed")
-    ws_bytes = ws.numel() * ws.element_size()
+        ws_bytes = ws.numel() * ws.element_size()
+        if ws_bytes < pl.need:
+            raise ValueError(f"decode workspace of {ws_bytes} bytes, {pl.need} needed")
     if out is None:
-        out3 = torch.empty(pl.out_shape, dtype=pl.out_dtype, device=q.device)
+        out3 = torch.empty_like(q)
     else:
-        out3 = out[:, 0] if out.dim() == 4 else out
+        out3 = out
     if pl.bt_copy:
         block_tables = block_tables.contiguous()
     if pl.ctx_copy:
         context_lens = context_lens.contiguous()
-    lib = _lib.load()
-    q_st, o_st = q3.stride(), out3.stride()
+    lib = _lib.calls()
+    q_st, o_st = pl.q_st, pl.out_st
     if pl.fp8:
         st = lib.nia_paged_decode_fp8(
-            out3.data_ptr(), o_st[0], o_st[1], q3.data_ptr(), q_st[0], q_st[1],
+            out3.data_ptr(), o_st[0], o_st[1], q.data_ptr(), q_st[0], q_st[1],
             k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
-            block_tables.data_ptr(), block_tables.stride(0), pl.max_blocks,
+            block_tables.data_ptr(), pl.bt_st, pl.max_blocks,
             context_lens.data_ptr(), pl.b, pl.h, pl.hkv, pl.d, pl.bs, pl.nb, pl.scale,
             ws.data_ptr(), ws_bytes, stream,
         )
@@ -397,17 +416,15 @@ def paged_decode(
             _lib.check("nia_paged_decode_fp8", st)
     else:
         st = lib.nia_paged_decode(
-            out3.data_ptr(), o_st[0], o_st[1], q3.data_ptr(), q_st[0], q_st[1],
+            out3.data_ptr(), o_st[0], o_st[1], q.data_ptr(), q_st[0], q_st[1],
             k_cache.data_ptr(), v_cache.data_ptr(),
-            block_tables.data_ptr(), block_tables.stride(0), pl.max_blocks,
+            block_tables.data_ptr(), pl.bt_st, pl.max_blocks,
             context_lens.data_ptr(), pl.b, pl.h, pl.hkv, pl.d, pl.bs, pl.nb, pl.scale,
             ws.data_ptr(), ws_bytes, pl.dt, stream,
         )
         if st:
             _lib.check("nia_paged_decode", st)
-    if out is not None:
-        return out
-    return out3.unsqueeze(1) if pl.squeeze else out3
+    return out3
 
 
 # ---------------------------------------------------------------------------------
@@ -466,7 +483,7 @@ def prefill(
     elif out.shape != q.shape or out.dtype != q.dtype:
         raise ValueError("out must match q's shape and dtype")
     _last_contig("out", out)
-    lib = _lib.load()
+    lib = _lib.calls()
     st = lib.nia_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
@@ -588,7 +605,7 @@ def prefill_paged(
     elif out.shape != q.shape or out.dtype != q.dtype:
         raise ValueError("out must match q's shape and dtype")
     _last_contig("out", out)
-    lib = _lib.load()
+    lib = _lib.calls()
     st = lib.nia_prefill_paged(
         out.data_ptr(), out.stride(0), out.stride(1),
         q.data_ptr(), q.stride(0), q.stride(1),
@@ -732,6 +749,16 @@ def _qk_plan(q, k, v, q_norm_weight, k_norm_weight, eps, positions, inv_freq, mr
     return pl
 
 
+def _inv_freq_f32(inv_freq: torch.Tensor) -> torch.Tensor:
+    """The RoPE table as contiguous fp32, converted once per table: a module cast to the
+    model dtype holds a rounded table, which every layer of every step passes."""
+    t = _INV_FREQ_F32.get(inv_freq, "f32")
+    if t is None:
+        t = inv_freq.to(torch.float32).contiguous()
+        _INV_FREQ_F32.put(inv_freq, "f32", t)
+    return t
+
+
 def qk_norm_rope_kv_write(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -789,7 +816,7 @@ def qk_norm_rope_kv_write(
             _QK_PLANS.clear()
         _QK_PLANS[sig] = pl
     pos = positions.to(torch.int64).contiguous() if pl.pos_copy else positions
-    inv = inv_freq.to(torch.float32).contiguous() if pl.inv_copy else inv_freq
+    inv = _inv_freq_f32(inv_freq) if pl.inv_copy else inv_freq
     qw, kw = q_norm_weight, k_norm_weight
     if pl.w_copy:
         qw, kw = qw.contiguous(), kw.contiguous()
@@ -799,7 +826,7 @@ def qk_norm_rope_kv_write(
     if pl.write:
         slots = slot_mapping.contiguous() if pl.slot_copy else slot_mapping
         kc_ptr, vc_ptr, sl_ptr = k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr()
-    lib = _lib.load()
+    lib = _lib.calls()
     args = (q.data_ptr(), pl.q_tok, pl.q_head, k.data_ptr(), pl.k_tok, pl.k_head,
             v.data_ptr(), pl.v_tok, pl.v_head,
             qw.data_ptr() if nw else None, kw.data_ptr() if nw else None,

@@ -208,6 +208,35 @@ def test_four_dim_query_and_explicit_scale():
     assert_attn_close(out4[:, 0], oracle_decode(c, scale=0.05), torch.float32, "scale 0.05")
 
 
+def test_query_layouts_and_the_output_layout_they_give():
+    """The same queries in several layouts give bit-identical results: (B, H, D), (B, 1, H, D)
+    (output (B, 1, H, D)), rows with gaps (output contiguous) and a head-major permutation
+    (output in the same layout); a given `out` of either rank is filled in place."""
+    c = workloads.make_decode(6, 16, 8, 128, [5, 70, 300, 1, 129, 64], 64, 16, torch.bfloat16,
+                              "cuda", seed=31)
+    ops.kv_write(c.k_new, c.v_new, c.k_cache[0], c.v_cache[0], c.slot_mapping)
+    args = (c.k_cache[0], c.v_cache[0], c.block_tables, c.context_lens)
+    base = ops.paged_decode(c.q, *args)
+    out4 = ops.paged_decode(c.q.unsqueeze(1), *args)
+    wide = torch.zeros(6, 16, 192, dtype=torch.bfloat16, device="cuda")
+    wide[..., :128] = c.q
+    gapped = ops.paged_decode(wide[..., :128], *args)
+    head_major = c.q.transpose(0, 1).contiguous().transpose(0, 1)
+    permuted = ops.paged_decode(head_major, *args)
+    given3 = torch.empty_like(c.q)
+    given4 = torch.empty(6, 1, 16, 128, dtype=torch.bfloat16, device="cuda")
+    r3 = ops.paged_decode(c.q, *args, out=given3)
+    r4 = ops.paged_decode(c.q.unsqueeze(1), *args, out=given4)
+    torch.cuda.synchronize()
+    assert base.shape == (6, 16, 128) and base.is_contiguous()
+    assert out4.shape == (6, 1, 16, 128) and torch.equal(out4[:, 0], base)
+    assert gapped.is_contiguous() and torch.equal(gapped, base)
+    assert permuted.stride() == head_major.stride() and torch.equal(permuted, base)
+    assert r3 is given3 and torch.equal(given3, base)
+    assert r4 is given4 and torch.equal(given4[:, 0], base)
+    assert_attn_close(base, oracle_decode(c), torch.bfloat16, "layouts")
+
+
 def test_one_workspace_shared_by_every_path_and_a_graph():
     """One workspace shared by bf16 calls of several batch sizes (the LDS-indexed and the
     large-batch prologue), an fp32 call (whose partitions overwrite the partial region)

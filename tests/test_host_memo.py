@@ -56,3 +56,24 @@ def test_varlen_max_seqlen_memo():
     assert ops._MAX_SEQLEN.get(cu, "max") == 7
     cu[1] = 6
     assert ops._MAX_SEQLEN.get(cu, "max") is None
+
+
+def test_rope_table_converted_once_per_table_and_again_after_a_change():
+    table = (1.0 / 10000 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128)).to(
+        torch.bfloat16)
+    first = ops._inv_freq_f32(table)
+    assert first.dtype == torch.float32 and first.is_contiguous()
+    assert torch.equal(first, table.float())
+    assert ops._inv_freq_f32(table) is first          # the same table: no new conversion
+    table.mul_(2)                                      # an in-place change: converted again
+    again = ops._inv_freq_f32(table)
+    assert again is not first and torch.equal(again, table.float())
+    other = table.clone()                              # another tensor with equal values
+    assert ops._inv_freq_f32(other) is not again
+
+
+def test_rope_tables_of_every_layer_stay_converted():
+    """A model holds one table per layer; all of them stay in the memo."""
+    tables = [torch.full((64,), 1.0 + i, dtype=torch.bfloat16) for i in range(64)]
+    first = [ops._inv_freq_f32(t) for t in tables]
+    assert all(ops._inv_freq_f32(t) is f for t, f in zip(tables, first))
