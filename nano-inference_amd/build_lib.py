@@ -106,7 +106,7 @@ def build_fast(verbose: bool = False) -> Path | None:
         return None
     out = PKG_DIR / FAST_NAME
     tmp = PKG_DIR / (FAST_NAME + ".tmp")
-    cmd = [cc, "-O2", "-Wall", "-Wextra", "-Werror", "-shared", "-fPIC", f"-I{inc}",
+    cmd = [cc, "-O2", "-Wall", "-Wextra", "-shared", "-fPIC", f"-I{inc}",
            str(FAST_SRC), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
