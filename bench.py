@@ -371,8 +371,8 @@ def _median_ms(fn, runs: int, budget_s: float) -> float:
 def cpu_baseline(torch, workloads, budget_s: float = 20.0):
     """The reference's attention, op for op on the host cores (the oracle's restatement of
     layers/attention.py:12-50 and :267-332 and layers/vision.py:190-208), fp32, with the
-    KV write loop and the attention timed apart: config 1 in full, and the decode, causal
-    prefill and vision workloads on stated subsets (their padded fp32 scores would not
+    KV write loop and the attention timed apart: the small fp32 decode in full, and the
+    Qwen3-8B decode, causal prefill and Qwen2.5-VL workloads on stated subsets (their padded fp32 scores would not
     fit or would take minutes).  One warm-up run, then the median of >= 5 runs.  The
     headline ``value`` is the decode subset's step (write + attention) in the units of
     the GPU line."""
@@ -400,16 +400,16 @@ def cpu_baseline(torch, workloads, budget_s: float = 20.0):
 
     legs = {}
     c1 = workloads.decode_small("cpu", torch.float32, 1001)
-    legs["config1_decode_full"] = dict(
-        decode_leg(c1, 9), what="config 1 in full: batch 4, 16/8 heads, D 128, contexts "
-                                f"{c1.lens}, block 16")
+    legs["decode_small_full"] = dict(
+        decode_leg(c1, 9), what="the small fp32 decode in full: batch 4, 16/8 heads, D 128, "
+                                f"contexts {c1.lens}, block 16")
     lens2 = workloads.uniform_lengths(64, 512, 8192, 2002)[:8]
     pool = sum(math.ceil(L / 16) for L in lens2) + 64
     c2 = workloads.make_decode(8, 32, 8, 128, lens2, pool, 16, torch.float32, "cpu", 2002)
-    legs["config2_decode_subset"] = dict(
-        decode_leg(c2, 5), what=f"config 2, its first 8 sequences (contexts {lens2}), 32/8 "
-                                "heads, D 128")
-    # causal prefill: the shortest of config 3's sequences, through the reference's prefill
+    legs["decode_qwen3_8b_subset"] = dict(
+        decode_leg(c2, 5), what=f"the Qwen3-8B decode (batch 64), its first 8 sequences "
+                                f"(contexts {lens2}), 32/8 heads, D 128")
+    # causal prefill: the shortest of the 8 sequences, through the reference's prefill
     # branch (write loop over the step's tokens, repeat_interleave, causal sdpa)
     lens3 = workloads.uniform_lengths(8, 256, 4096, 3003)
     L3 = min(lens3)
@@ -423,10 +423,11 @@ def cpu_baseline(torch, workloads, budget_s: float = 20.0):
     w3 = _median_ms(lambda: ref.kv_write_loop(k3, v3, kc3, vc3, slots3), 5, each / 4)
     a3 = _median_ms(lambda: ref.paged_attention(q3, k3, v3, kc3, vc3, none3, None, None, None,
                                                 is_prefill=True), 5, each)
-    legs["config3_prefill_subset"] = dict(
+    legs["prefill_qwen3_8b_subset"] = dict(
         write_ms=round(w3, 3), attention_ms=round(a3, 3),
         attention_gflops=round(c3.flops() / (a3 * 1e-3) / 1e9, 2),
-        what=f"config 3, its shortest sequence ({L3} tokens of {lens3}), causal, 32/8 heads")
+        what=f"the Qwen3-8B causal prefill, its shortest sequence ({L3} tokens of {lens3}), "
+             "32/8 heads")
     # vision: the first image (28 x 28 patches), full attention and its 64-token windows
     grid = [workloads.VISION_GRIDS[0]]
     cu_full = vw.full_cu_seqlens(grid)
@@ -438,22 +439,24 @@ def cpu_baseline(torch, workloads, budget_s: float = 20.0):
     fl_win = 4 * 16 * 80 * sum(x * x for x in wl)
     af = _median_ms(lambda: ref.vision_attention(c5.q, c5.k, c5.v, cu_full), 5, each / 2)
     aw = _median_ms(lambda: ref.vision_attention(c5.q, c5.k, c5.v, cu_win), 5, each / 2)
-    legs["config5_vision_subset"] = dict(
+    legs["vision_qwen25vl_subset"] = dict(
         full_ms=round(af, 3), full_gflops=round(fl_full / (af * 1e-3) / 1e9, 2),
         window_ms=round(aw, 3), window_gflops=round(fl_win / (aw * 1e-3) / 1e9, 2),
-        what=f"config 5, its first image ({grid[0][1]}x{grid[0][2]} patches, {S5} tokens), "
+        what=f"the Qwen2.5-VL vision tower, its first image ({grid[0][1]}x{grid[0][2]} "
+             f"patches, {S5} tokens), "
              f"16 heads, D 80: full attention and its {len(wl)} windows")
     lensv = workloads.uniform_lengths(32, 1024, 6144, 5005)[:4]
     poolv = sum(math.ceil(L / 16) for L in lensv) + 64
     cv = workloads.make_decode(4, 28, 4, 128, lensv, poolv, 16, torch.float32, "cpu", 5005)
-    legs["config5_decode_subset"] = dict(
-        decode_leg(cv, 5), what=f"config 5 language decode, its first 4 sequences (contexts "
-                                f"{lensv}), 28/4 heads, D 128")
-    head = legs["config2_decode_subset"]
+    legs["decode_qwen25vl_subset"] = dict(
+        decode_leg(cv, 5), what=f"the Qwen2.5-VL language decode (batch 32), its first 4 "
+                                f"sequences (contexts {lensv}), 28/4 heads, D 128")
+    head = legs["decode_qwen3_8b_subset"]
     return dict(value=head["step_gbps"], unit="GB/s", cores=torch.get_num_threads(),
                 kind="port", cpu_model=_cpu_model(), threads=torch.get_num_threads(),
                 sample=("reference decode step (per-token KV write loop + padded gather, "
-                        "repeat_interleave, fp32 softmax) on config 2's first 8 sequences, fp32; "
+                        "repeat_interleave, fp32 softmax) on the first 8 sequences of the "
+                        "Qwen3-8B decode, fp32; "
                         "bytes counted at fp32 element size; the other legs as listed"),
                 legs=legs)
 

@@ -591,8 +591,8 @@ class MixedGenerator:
         return st
 
 
-def config4_prompts(num_requests: int = 64, lo: int = 128, hi: int = 2048,
-                    vocab: int = 151936, seed: int = 4004) -> List[List[int]]:
+def generation_prompts(num_requests: int = 64, lo: int = 128, hi: int = 2048,
+                       vocab: int = 151936, seed: int = 4004) -> List[List[int]]:
     """64 prompts of U[128, 2048] token ids drawn U[0, vocab), seeded."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     lens = torch.randint(lo, hi + 1, (num_requests,), generator=g).tolist()
@@ -608,7 +608,7 @@ def build(cfg: Optional[Qwen3Config] = None, prompts: Optional[List[List[int]]] 
     ``MixedGenerator`` (chunked prefill mixed with decodes) when ``mixed``, else the
     prefill-first ``Generator``; ``fp8_cache`` keeps the KV pool in the fp8 format."""
     cfg = cfg or Qwen3Config()
-    prompts = prompts if prompts is not None else config4_prompts(seed=seed)
+    prompts = prompts if prompts is not None else generation_prompts(seed=seed)
     model = Qwen3ForCausalLM(cfg).init_random(seed).to(device=device, dtype=dtype).eval()
     need = sum(math.ceil((len(p) + max_new_tokens) / block_size) for p in prompts)
     pool = KVPool(cfg, need + 16, block_size, dtype, torch.device(device), fp8=fp8_cache)
@@ -723,7 +723,7 @@ def main() -> int:
     ap.add_argument("--fp8-cache", action="store_true", help="KV pool in the fp8 format")
     args = ap.parse_args()
     cfg = Qwen3Config(num_layers=args.layers)
-    gen = build(cfg, config4_prompts(args.requests), args.max_new_tokens,
+    gen = build(cfg, generation_prompts(args.requests), args.max_new_tokens,
                 max_prefill_batch=args.prefill_batch, use_graph=not args.eager,
                 mixed=args.mixed, max_step_tokens=args.step_tokens, chunk=args.chunk,
                 fp8_cache=args.fp8_cache)

@@ -49,9 +49,9 @@ def test_decode_metadata_matches_context_builder():
         assert torch.equal(gen._bt, ref["kv_block_tables"])
 
 
-def test_config4_prompts_are_seeded():
-    a = e2e.config4_prompts(8, 128, 2048, seed=4004)
-    b = e2e.config4_prompts(8, 128, 2048, seed=4004)
+def test_generation_prompts_are_seeded():
+    a = e2e.generation_prompts(8, 128, 2048, seed=4004)
+    b = e2e.generation_prompts(8, 128, 2048, seed=4004)
     assert a == b
     assert all(128 <= len(p) <= 2048 for p in a)
     assert all(0 <= t < 151936 for p in a for t in p)

@@ -47,7 +47,7 @@ def check_teacher_forcing(gen, prompts, new):
 @pytest.mark.parametrize("prefill_batch", [1, 3])
 def test_generation_matches_dense_recompute(prefill_batch):
     cfg = tiny_config()
-    prompts = e2e.config4_prompts(5, 3, 70, cfg.vocab_size, seed=11)
+    prompts = e2e.generation_prompts(5, 3, 70, cfg.vocab_size, seed=11)
     new = 7
     gen = e2e.build(cfg, prompts, max_new_tokens=new, max_prefill_batch=prefill_batch, seed=5)
     st = gen.run(prompts)
@@ -62,7 +62,7 @@ def test_mixed_generation_matches_dense_recompute(step_tokens, chunk):
     """Chunked prefill mixed with decodes (packed steps): the chunks attend through
     the paged cache, decode rows through the decode kernel, in the same steps."""
     cfg = tiny_config()
-    prompts = e2e.config4_prompts(6, 3, 90, cfg.vocab_size, seed=12)
+    prompts = e2e.generation_prompts(6, 3, 90, cfg.vocab_size, seed=12)
     new = 7
     gen = e2e.build(cfg, prompts, max_new_tokens=new, seed=5, mixed=True,
                     max_step_tokens=step_tokens, chunk=chunk)
@@ -75,7 +75,7 @@ def test_mixed_generation_matches_dense_recompute(step_tokens, chunk):
 
 def test_kv_pool_blocks_are_returned():
     cfg = tiny_config()
-    prompts = e2e.config4_prompts(3, 10, 40, cfg.vocab_size, seed=3)
+    prompts = e2e.generation_prompts(3, 10, 40, cfg.vocab_size, seed=3)
     gen = e2e.build(cfg, prompts, max_new_tokens=3, max_prefill_batch=2, seed=1)
     free0 = len(gen.pool.free)
     gen.run(prompts)
@@ -86,7 +86,7 @@ def test_graph_decode_reproduces_eager_decode():
     """The captured decode step, replayed with eager work and a sync between replays,
     yields the eager loop's tokens exactly (same kernels, same order)."""
     cfg = tiny_config()
-    prompts = e2e.config4_prompts(6, 5, 90, cfg.vocab_size, seed=21)
+    prompts = e2e.generation_prompts(6, 5, 90, cfg.vocab_size, seed=21)
     eager = e2e.build(cfg, prompts, max_new_tokens=9, max_prefill_batch=4, seed=9)
     eager.run(prompts)
     graph = e2e.build(cfg, prompts, max_new_tokens=9, max_prefill_batch=4, seed=9,
@@ -107,7 +107,7 @@ def test_mixed_graph_tail_reproduces_eager_tail():
     """The mixed generator's captured decode tail, replayed with eager work and a
     sync between replays, yields the eager tail's tokens exactly."""
     cfg = tiny_config()
-    prompts = e2e.config4_prompts(6, 5, 90, cfg.vocab_size, seed=22)
+    prompts = e2e.generation_prompts(6, 5, 90, cfg.vocab_size, seed=22)
     kw = dict(max_new_tokens=9, seed=9, mixed=True, max_step_tokens=40, chunk=16)
     eager = e2e.build(cfg, prompts, use_graph=False, **kw)
     eager.run(prompts)
@@ -130,7 +130,7 @@ def test_generation_with_fp8_cache(mixed):
     comes from attention over the fresh K/V, so it equals the bf16 pool's exactly; the
     rest read the fp8 cache (its parity is checked at the layer and kernel level)."""
     cfg = tiny_config()
-    prompts = e2e.config4_prompts(5, 3, 70, cfg.vocab_size, seed=13)
+    prompts = e2e.generation_prompts(5, 3, 70, cfg.vocab_size, seed=13)
     kw = dict(max_new_tokens=6, seed=5, mixed=mixed, max_step_tokens=48, chunk=16)
     ref_gen = e2e.build(cfg, prompts, **kw)
     ref_gen.run(prompts)

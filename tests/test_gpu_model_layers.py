@@ -337,7 +337,7 @@ def _qwen3_0p6b_two_layers():
 @pytest.mark.parametrize("mixed", [False, True])
 def test_generation_qwen3_0p6b_shape_matches_float64_model(mixed):
     cfg = _qwen3_0p6b_two_layers()
-    prompts = e2e.config4_prompts(5, 20, 90, cfg.vocab_size, seed=31)
+    prompts = e2e.generation_prompts(5, 20, 90, cfg.vocab_size, seed=31)
     new = 6
     gen = e2e.build(cfg, prompts, max_new_tokens=new, max_prefill_batch=3, seed=7, mixed=mixed,
                     max_step_tokens=96, chunk=32)

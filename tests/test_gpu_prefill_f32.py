@@ -35,7 +35,7 @@ def check(out, q, k, v, qs, ql, ks, kl, mode, what):
     assert_attn_close(got, exp, F32, what)
 
 
-def test_causal_config1_layout():
+def test_causal_small_batch_layout():
     """16/8 heads, D 128, sequences of 17, 64, 200 and 511 tokens (the fp32 decode
     workload's lengths, as a causal prefill), every row."""
     lens = [17, 64, 200, 511]
@@ -43,7 +43,7 @@ def test_causal_config1_layout():
     out = ops.varlen_attention(c.q, c.k, c.v, c.cu_seqlens, causal=True)
     torch.cuda.synchronize()
     cu = c.cu_seqlens.tolist()
-    check(out, c.q, c.k, c.v, cu[:-1], lens, cu[:-1], lens, "top_left", "fp32 causal config-1")
+    check(out, c.q, c.k, c.v, cu[:-1], lens, cu[:-1], lens, "top_left", "fp32 causal, small batch")
 
 
 @pytest.mark.parametrize("head_dim", [64, 80, 96, 128])

@@ -6,7 +6,7 @@ src/nano_inference/engine/context_builder.py:83-193 and :18-81, pinned by the
 reference's known answers (tests/test_context_builder_host.py).  Cases: those known
 answers, seeded mixed prefill / recompute / decode batches at block sizes 4 and 16,
 tables that end before the last position (the builder falls back to the last
-block, as the reference does), mRoPE batches, one decode row, and a config-4-sized
+block, as the reference does), mRoPE batches, one decode row, and a Qwen3-0.6B-generation-sized
 prefill batch (8 prompts up to 2048 tokens).
 """
 import pytest
@@ -62,7 +62,7 @@ def test_mrope_batches(seed):
     check(random_batch(200 + seed, 9, mrope=True))
 
 
-def test_config4_prefill_batch():
+def test_generation_sized_prefill_batch():
     g = torch.Generator().manual_seed(4004)
     qs = []
     perm = torch.randperm(40000, generator=g).tolist()
