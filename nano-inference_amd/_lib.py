@@ -164,11 +164,28 @@ def load() -> C.CDLL:
     return _lib
 
 
+# Argument kind letters of _nia_fast (p pointer, l int64, i int32, f float, z size_t).
+_KIND_LETTER = {_p: "p", _i64: "l", _i32: "i", _f32: "f", _sz: "z"}
+
+
+def fast_kinds(name: str) -> str:
+    """The argument kinds _nia_fast must use for ``name``, from ``SIGNATURES``."""
+    return "".join(_KIND_LETTER[a] for a in SIGNATURES[name][1])
+
+
 def fast_module():
-    """The _nia_fast extension module, or None where it has not been built."""
+    """The _nia_fast extension module, or None where it has not been built or was built
+    for other signatures than ``SIGNATURES`` (a stale build: its calls would pass the
+    arguments in the wrong layout, so the ctypes binding is used instead)."""
     try:
         from . import _nia_fast
     except ImportError:
+        return None
+    kinds = getattr(_nia_fast, "kinds", {})
+    if any(kinds.get(name) != fast_kinds(name) for name in FAST_CALLS):
+        import warnings
+        warnings.warn("_nia_fast does not match the library's signatures (rebuild it with "
+                      "build_lib.py); the hot calls go through ctypes", RuntimeWarning)
         return None
     return _nia_fast
 

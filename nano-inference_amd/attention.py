@@ -291,7 +291,7 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
             if s == 1:
                 # 2b. Decode: gather + GQA + mask + softmax in one kernel (:285-332).
                 attn = ops.paged_decode(q[:, 0], k_cache, v_cache, bt, ctx, k_scale=ks,
-                                        v_scale=vs)
+                                        v_scale=vs, workspace=metadata.decode_workspace)
             else:
                 # 2c. Several new tokens on top of cached context: chunked prefill.
                 dev = x.device
@@ -320,7 +320,8 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         n = md.q_start.shape[0]
         if nd > 0:
             ops.paged_decode(q2[:nd], k_cache, v_cache, md.kv_block_tables[:nd],
-                             md.context_lens[:nd], out=out[:nd], k_scale=ks, v_scale=vs)
+                             md.context_lens[:nd], out=out[:nd], k_scale=ks, v_scale=vs,
+                             workspace=md.decode_workspace)
         if nd < n:
             ops.prefill_paged(q2, k_cache, v_cache, md.kv_block_tables[nd:], md.q_start[nd:],
                               md.q_len[nd:], md.context_lens[nd:], md.max_q_len,

@@ -100,11 +100,13 @@ def build_fast(verbose: bool = False) -> Path | None:
     """
     cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
     inc = sysconfig.get_paths().get("include")
+    out = PKG_DIR / FAST_NAME
     if not cc or not inc or not (Path(inc) / "Python.h").exists():
+        # An earlier build would be bound to the new library without matching it.
+        out.unlink(missing_ok=True)
         print(f"warning: {FAST_NAME} not built (no C compiler or Python.h); "
               "the hot calls go through ctypes", file=sys.stderr)
         return None
-    out = PKG_DIR / FAST_NAME
     tmp = PKG_DIR / (FAST_NAME + ".tmp")
     cmd = [cc, "-O2", "-Wall", "-Wextra", "-shared", "-fPIC", f"-I{inc}",
            str(FAST_SRC), "-o", str(tmp)]

@@ -17,7 +17,8 @@ import torch
 @dataclass
 class AttentionMetadata:
     """Metadata required for paged attention: the reference's fields in its order,
-    plus the optional row scales of fp8 caches (default None)."""
+    plus the optional row scales of fp8 caches and an optional caller-owned decode
+    workspace (default None)."""
 
     context_lens: torch.Tensor  # (B,) int64 - total sequence length per request
     kv_block_tables: torch.Tensor  # (B, max_blocks_per_seq) int32, zero-padded
@@ -37,6 +38,12 @@ class AttentionMetadata:
     # block_size] float32 beside uint8 / float8_e4m3fn k_cache / v_cache.
     k_scale: Optional[torch.Tensor] = None
     v_scale: Optional[torch.Tensor] = None
+
+    # Not in the reference: a caller-owned decode workspace (uint8, at least
+    # ops.decode_workspace_bytes(...) for the step's sizes) for decode calls that are
+    # captured in a HIP graph, so that the graph holds memory its owner controls; None
+    # uses the per-stream workspace of ops.decode_workspace.
+    decode_workspace: Optional[torch.Tensor] = None
 
 
 @dataclass

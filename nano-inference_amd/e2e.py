@@ -168,6 +168,16 @@ class KVPool:
         self.free.extend(blocks)
 
 
+def _graph_workspace(model, pool: KVPool, block_tables: torch.Tensor) -> torch.Tensor:
+    """A decode workspace owned by the generator for the decode steps it captures in a HIP
+    graph (batch and table width fixed), released with the graph when the run ends."""
+    cfg = model.config
+    qdt = torch.bfloat16 if pool.k_scale is not None else pool.k_cache.dtype
+    n = ops.decode_workspace_bytes(block_tables.shape[0], cfg.num_heads, cfg.num_kv_heads,
+                                   block_tables.shape[1], pool.block_size, cfg.head_dim, qdt)
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=block_tables.device)
+
+
 @dataclass
 class _Seq:
     prompt: List[int]
@@ -275,6 +285,7 @@ class Generator:
             self._hist = torch.zeros((b, self.max_new), dtype=torch.int64, device=dev)
             self._hist[:, 0] = torch.stack([s.generated[0] for s in running]).to(torch.int64)
             self._step = torch.ones(1, dtype=torch.int64, device=dev)  # index being produced
+            self._ws = _graph_workspace(self.model, self.pool, self._bt)
             self._decode_step()  # eager first step (also warms up the libraries)
             st.decode_steps += 1
             if self.use_graph and self.max_new > 2:
@@ -318,7 +329,8 @@ class Generator:
         md = AttentionMetadata(context_lens=ctx, kv_block_tables=self._bt,
                                slot_mapping=slot.unsqueeze(1), k_cache=self.pool.k_cache,
                                v_cache=self.pool.v_cache, k_scale=self.pool.k_scale,
-                               v_scale=self.pool.v_scale, is_prefill=False)
+                               v_scale=self.pool.v_scale, is_prefill=False,
+                               decode_workspace=self._ws)
         logits = self.model(tok, p.unsqueeze(1), None, md, self._zero)
         nxt = torch.argmax(logits, dim=-1, keepdim=True)
         self._hist.scatter_(1, self._step.expand(self._hist.shape[0], 1), nxt)
@@ -457,6 +469,7 @@ class MixedGenerator:
         self._rows = torch.arange(b, device=dev)
         self._zero = torch.zeros(b, dtype=torch.int64, device=dev)
         self._spare = torch.full((b,), self._tok.numel() - 1, dtype=torch.int64, device=dev)
+        self._ws = _graph_workspace(self.model, self.pool, self._bt)
         self._tail_step()
         st.decode_steps += 1
         if left > 1:
@@ -487,7 +500,8 @@ class MixedGenerator:
         md = AttentionMetadata(context_lens=p + 1, kv_block_tables=self._bt,
                                slot_mapping=slot.unsqueeze(1), k_cache=self.pool.k_cache,
                                v_cache=self.pool.v_cache, k_scale=self.pool.k_scale,
-                               v_scale=self.pool.v_scale, is_prefill=False)
+                               v_scale=self.pool.v_scale, is_prefill=False,
+                               decode_workspace=self._ws)
         logits = self.model(tok.unsqueeze(1), p.unsqueeze(1), None, md, self._zero)
         live = self._prod < self.max_new
         dst = torch.where(live, self._sid * self.max_new + self._prod, self._spare)

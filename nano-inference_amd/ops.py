@@ -232,8 +232,12 @@ def check_decode_shape(head_dim: int, block_size: int, num_heads: int, num_kv_he
 # One workspace per (device, stream): calls on one stream run one after another and may
 # share it; calls on other streams get their own.  A workspace that is outgrown is kept
 # (in _RETIRED) rather than freed, since a captured HIP graph may still hold its address.
+# Workspaces grow geometrically (at least twice the outgrown size), so the retired ones of
+# a stream add up to less than its live one; release_retired_workspaces() frees them once
+# the caller knows that no graph holding them will be replayed.
 _DECODE_WS: dict = {}
 _RETIRED: list = []
+_MIN_WS_BYTES = 1 << 20
 
 
 def decode_workspace(device: torch.device, nbytes: int, stream=None) -> torch.Tensor:
@@ -249,11 +253,28 @@ def decode_workspace(device: torch.device, nbytes: int, stream=None) -> torch.Te
     key = (dev.index if dev.type == "cuda" else -1, handle)
     ws = _DECODE_WS.get(key)
     if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, _MIN_WS_BYTES)
         if ws is not None:
             _RETIRED.append(ws)
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            size = max(size, 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=dev)
         _DECODE_WS[key] = ws
     return ws
+
+
+def retired_workspace_bytes() -> int:
+    """Bytes held by outgrown decode workspaces (kept for graphs that may hold them)."""
+    return sum(t.numel() for t in _RETIRED)
+
+
+def release_retired_workspaces() -> int:
+    """Free the outgrown decode workspaces and return their total size in bytes.  Call it
+    only when no captured HIP graph that ran paged_decode before the growth will be
+    replayed again (for example after deleting such graphs): a replay would write to
+    freed memory."""
+    n = retired_workspace_bytes()
+    _RETIRED.clear()
+    return n
 
 
 class _DecodePlan:
@@ -371,7 +392,7 @@ def paged_decode(
            block_tables.get_device(),
            context_lens.shape, context_lens.stride(), context_lens.dtype,
            context_lens.get_device(), scale,
-           None if out is None else (out.shape, out.stride(), out.dtype),
+           None if out is None else (out.shape, out.stride(), out.dtype, out.get_device()),
            None if k_scale is None else (k_scale.shape, k_scale.stride(), k_scale.dtype,
                                          k_scale.get_device()),
            None if v_scale is None else (v_scale.shape, v_scale.stride(), v_scale.dtype,
@@ -391,6 +412,8 @@ def paged_decode(
         ws_bytes = ws.numel()  # uint8
     else:
         ws = workspace
+        if ws.get_device() != dq:
+            raise ValueError(f"decode workspace on {ws.device}, q on {q.device}")
         ws_bytes = ws.numel() * ws.element_size()
         if ws_bytes < pl.need:
             raise ValueError(f"decode workspace of {ws_bytes} bytes, {pl.need} needed")

@@ -29,6 +29,19 @@ def test_argument_kinds_follow_the_ctypes_signatures(fast):
         assert fast.kinds[name] == "".join(KIND[a] for a in args), name
 
 
+def test_a_module_built_for_other_signatures_is_not_used(fast, monkeypatch):
+    """A stale _nia_fast (argument kinds that no longer match SIGNATURES) must not be
+    bound: its calls would pass the arguments in the wrong layout."""
+    stale = dict(fast.kinds)
+    stale["nia_paged_decode"] = stale["nia_paged_decode"][:-1]  # one argument fewer
+    monkeypatch.setattr(fast, "kinds", stale)
+    with pytest.warns(RuntimeWarning, match="does not match"):
+        assert _lib.fast_module() is None
+    monkeypatch.setattr(fast, "kinds", dict(fast.kinds, nia_prefill="p" * 25))
+    with pytest.warns(RuntimeWarning):
+        assert _lib.fast_module() is None
+
+
 P = 16  # a pointer value validation rejects before any use
 
 

@@ -104,10 +104,11 @@ def test_long_contexts_and_a_zeroed_context():
 
 @pytest.mark.parametrize("batch", [1024, 1025])
 @pytest.mark.parametrize("heads", [16, 28])
-def test_groups_at_the_staged_batch_limit(heads, batch):
-    """bf16 batches of up to 1024 sequences run the matrix-core loop (block pairs staged
-    through LDS); above it groups of 4 take the register pipeline and groups of 7 the
-    plain vector loop.  Short contexts (1 to 40 tokens) keep the oracle quick."""
+def test_groups_at_the_lds_prefix_batch_limit(heads, batch):
+    """bf16 batches of up to 1024 sequences build the split kernel's unit prefix in LDS
+    inside the kernel; above it decode_prefix_kernel writes the prefix to the workspace
+    first and the split kernel reads it from there.  Groups of 4 and 7, short contexts
+    (1 to 40 tokens) keep the oracle quick."""
     lens = [int(x) for x in torch.randint(1, 41, (batch,),
                                           generator=torch.Generator().manual_seed(batch))]
     c = workloads.make_decode(batch, heads, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",
@@ -128,7 +129,7 @@ def test_zero_context_gives_zeros():
 @pytest.mark.parametrize("heads", [16, 28])
 def test_block_table_permutation_is_bit_invariant(heads):
     """Moving every block to another physical id (and updating the table) changes nothing
-    (4 KV heads: groups of 4, register pipeline; of 7, block pairs staged through LDS)."""
+    (4 KV heads with groups of 4 and of 7, on the split kernel)."""
     c = workloads.make_decode(6, heads, 4, 128, [100, 700, 1600, 33, 512, 2049], 1024, 16,
                               torch.bfloat16, "cuda", 91)
     out1 = run_step(c)
@@ -293,3 +294,21 @@ def test_one_workspace_shared_by_every_path_and_a_graph():
         assert torch.equal(out, expected["a"])
         assert torch.equal(call(big, ws), expected["big"])  # eager work in between
         torch.cuda.synchronize()
+
+
+def test_out_or_workspace_off_the_device_raises_before_launch():
+    """A call whose plan is cached (same shapes and strides) but whose ``out`` or
+    ``workspace`` lies on the host raises ValueError instead of handing the kernel a host
+    pointer."""
+    c = workloads.make_decode(3, 8, 2, 128, [5, 40, 600], 64, 16, torch.bfloat16, "cuda", 78)
+    args = (c.q, c.k_cache[0], c.v_cache[0], c.block_tables, c.context_lens)
+    good = ops.paged_decode(*args, out=torch.empty_like(c.q))
+    with pytest.raises(ValueError, match="device"):
+        ops.paged_decode(*args, out=torch.empty(c.q.shape, dtype=c.q.dtype))
+    need = ops.decode_workspace_bytes(3, 8, 2, c.block_tables.shape[1], 16, 128)
+    with pytest.raises(ValueError, match="workspace"):
+        ops.paged_decode(*args, workspace=torch.empty(need, dtype=torch.uint8))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    again = ops.paged_decode(*args, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(good, again)

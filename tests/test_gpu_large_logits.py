@@ -8,8 +8,9 @@ so that logits reach ~100 nats:
   late   two dominant keys, one a third into the context and one at its end;
   fall   the first key dominates and the rest underflow;
   scaled q and k times 4 (logits ~N(0, 16^2)).
-Kernels: decode on the matrix-core loop (batch <= 1024) for groups of 1, 4 and 7, on
-the vector loops (batch 1025), in fp32 and over fp8 caches; causal, chunked, vision
+Kernels: decode on the split kernel with its unit prefix built in LDS (batch <= 1024)
+for groups of 1, 4 and 7 and with the prefix from decode_prefix_kernel (batch 1025), in
+fp32 and over fp8 caches; causal, chunked, vision
 full (D 80), paired-head windows and paired heads over many key tiles.
 Oracle: oracle.textbook in float64 (softmax(q K^T / sqrt(D)) V, the mathematics of
 src/nano_inference/layers/attention.py:12-50 and :285-332).

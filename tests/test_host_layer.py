@@ -30,12 +30,13 @@ def test_parameter_names_match_reference_layer():
 
 def test_metadata_fields_match_reference_dataclass():
     """The reference's fields in its order (core/context.py:7-24); the only additions are
-    the optional fp8 row scales, after them and defaulting to None."""
+    the optional fp8 row scales and the caller-owned decode workspace, after them and
+    defaulting to None."""
     fields = AttentionMetadata.__dataclass_fields__
     assert list(fields)[:7] == ["context_lens", "kv_block_tables", "slot_mapping", "k_cache",
                                 "v_cache", "is_prefill", "mrope_position_ids"]
-    assert list(fields)[7:] == ["k_scale", "v_scale"]
-    assert all(fields[f].default is None for f in ("k_scale", "v_scale"))
+    assert list(fields)[7:] == ["k_scale", "v_scale", "decode_workspace"]
+    assert all(fields[f].default is None for f in ("k_scale", "v_scale", "decode_workspace"))
 
 
 def test_ops_refuse_cpu_tensors():
