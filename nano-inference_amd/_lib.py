@@ -34,7 +34,7 @@ ERR_WORKSPACE = 3
 ERR_LAUNCH = 4
 ERR_MISALIGNED = 5
 ERR_SCRATCH_LIMIT = 6
-DECODE_SCRATCH_BYTES = 32 << 20  # NIA_DECODE_SCRATCH_BYTES
+DECODE_SCRATCH_BYTES = 40 << 20  # NIA_DECODE_SCRATCH_BYTES
 
 _p = C.c_void_p
 _i32 = C.c_int32
