@@ -97,7 +97,9 @@ int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
  *                own; calls issued one after another may share one.
  * Supported:
  *   dtype bf16 (fp32 softmax and accumulation): block_size a power of two >= 4,
- *     head_dim 64, 80, 96 or 128, num_heads / num_kv_heads in 1..16;
+ *     head_dim 64, 80, 96 or 128, any num_heads / num_kv_heads (groups of more than
+ *     16 query heads per KV head run as several launches of at most 16 heads each,
+ *     which share the workspace one after another on the stream);
  *   dtype f32 (q . k summed in fp64): any block_size, head_dim 64, 80, 96 or 128, any
  *     num_heads / num_kv_heads.
  */
@@ -177,9 +179,11 @@ int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
  * by nia_kv_write) and reads its keys [0, context_lens[s]) through
  * block_tables exactly as nia_paged_decode does.  `causal` is normally
  * NIA_CAUSAL_BOTTOM_RIGHT; NIA_CAUSAL_NONE lets every row see the whole context.
- * Supported: head_dim 64, 80, 96 or 128; dtype bf16 with block_size a power of two in
- * 1..64, or f32 with any block_size >= 1 (keys in blocks outside [0, num_blocks) are
- * skipped).
+ * Supported: head_dim 64, 80, 96 or 128; dtype bf16 with block_size a power of two
+ * (block sizes of 16 and more stream 16-row groups of a block into LDS by DMA, smaller
+ * ones take register-staged loads) and max_blocks_per_seq * block_size < 2^31, or f32
+ * with any block_size >= 1 (keys in blocks outside [0, num_blocks) are skipped).
+ * Other bf16 block sizes return NIA_ERR_UNSUPPORTED before anything is launched.
  */
 int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,
                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -281,8 +285,8 @@ int32_t nia_qk_norm_rope_kv_write_fp8(void* q, int64_t q_tok_stride, int64_t q_h
  * are dequantised exactly as code * row scale (the code is widened to bf16 without
  * rounding, the scale multiplies the q . k score, and each softmax weight carries its
  * row's v scale).  Same workspace contract as nia_paged_decode (its size with dtype
- * NIA_DTYPE_BF16); head_dim 128, block_size a power of two >= 16, num_heads /
- * num_kv_heads <= 16.
+ * NIA_DTYPE_BF16); head_dim 128, block_size a power of two >= 16, any num_heads /
+ * num_kv_heads (as nia_paged_decode).
  */
 int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride, int64_t out_head_stride,
                              const void* q, int64_t q_batch_stride, int64_t q_head_stride,

@@ -25,7 +25,8 @@
 //   last item, and with hg = 4 the 4 waves of a workgroup read the 4 adjacent KV heads
 //   of the same blocks (16 KB contiguous per block for K and for V).
 //   Shapes: block size a power of two >= 4 (>= 16 for fp8), head_dim 64 / 80 / 96 / 128
-//   (fp8: 128), G <= 16.
+//   (fp8: 128), any G: groups of more than 16 query heads per KV head run as launches of
+//   at most 16 heads each (the MFMA columns), one after another on the stream.
 // fp32 caches (the reference's CPU default; tolerance 1e-5):
 //   head_dim 128, block size 16, G <= 8: paged_decode_partial_kernel, grid (partition,
 //   KV head, sequence); wave w takes blocks w, w + 4, ... of the partition; 32 lanes per
@@ -75,7 +76,8 @@ struct DecodeParams {
   int32_t max_parts;
   // split kernel
   int32_t bs_log2;
-  int32_t group;  // G = num_heads / num_kv_heads
+  int32_t group;  // G = num_heads / num_kv_heads (split kernel: query heads of this launch per KV head)
+  int32_t q_group;  // split kernel: heads between KV head groups in q and out (the call's G)
   int32_t hg;     // KV heads per workgroup
   int32_t wph;    // slices per KV head (4 / hg)
   int32_t nhg;    // head groups (num_kv_heads / hg)
@@ -845,7 +847,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   auto load_q = [&](const SplitUnit& x, uint4 (&qv)[4], uint2& qt) __attribute__((always_inline)) {
     const int hk = x.g * hg + hig;
     const bf16_t* qp = reinterpret_cast<const bf16_t*>(p.q) + (int64_t)x.b * p.q_b +
-                       (int64_t)(hk * G + (hn < G ? hn : 0)) * p.q_h;
+                       (int64_t)(hk * p.q_group + (hn < G ? hn : 0)) * p.q_h;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
       const int d0 = FP8 ? 64 * (s >> 1) + 16 * quad + 8 * (s & 1) : 32 * s + 8 * quad;
@@ -872,7 +874,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     if (hn < G) {
       if (whole) {
         bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)x.b * p.out_b +
-                      (int64_t)(hk * G + hn) * p.out_h + 4 * quad;
+                      (int64_t)(hk * p.q_group + hn) * p.out_h + 4 * quad;
         const float inv = ls > 0.f ? 1.f / ls : 0.f;
 #pragma unroll
         for (int mt = 0; mt < kDt; ++mt)
@@ -1112,7 +1114,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
   const int n_units = p.ws_pfx[b + 1] - pb;
   const int d0 = 2 * lane;
   const bool has_dims = d0 < D;
-  bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b + (int64_t)h * p.out_h;
+  bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b +
+                (int64_t)(hk * p.q_group + gq) * p.out_h;
   if (n_units <= 0) {
     if (has_dims) *reinterpret_cast<uint32_t*>(out + d0) = 0u;
     return;
@@ -1197,14 +1200,20 @@ size_t split_pfx_bytes(int32_t batch) { return round_up((size_t)(batch + 1) * si
 // workgroup, for the largest grid.
 size_t split_rows(int32_t group) { return (size_t)kSplitMaxGrid * 8 * (size_t)group; }
 
+// Groups of more than kSplitMaxGroup query heads per KV head run as several launches of
+// at most kSplitMaxGroup heads each (the MFMA columns), one after another, sharing the
+// workspace.
+constexpr int kSplitMaxGroup = 16;
+
 size_t split_workspace(int32_t batch, int32_t group, int32_t head_dim) {
+  const int32_t g = group < kSplitMaxGroup ? group : kSplitMaxGroup;
   return kHeaderBytes + split_pfx_bytes(batch) +
-         split_rows(group) * ((size_t)head_dim + 2) * sizeof(float);
+         split_rows(g) * ((size_t)head_dim + 2) * sizeof(float);
 }
 
 bool split_shape(bool fp8, int32_t head_dim, int32_t block_size, int32_t group) {
   const bool pow2 = block_size > 0 && (block_size & (block_size - 1)) == 0;
-  if (!pow2 || block_size < (fp8 ? 16 : 4) || group < 1 || group > 16) return false;
+  if (!pow2 || block_size < (fp8 ? 16 : 4) || group < 1) return false;
   return fp8 ? head_dim == 128
              : (head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128);
 }
@@ -1440,18 +1449,35 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
   p.nhg = num_kv_heads / p.hg;
   p.ws_pfx = reinterpret_cast<int32_t*>(ws + kHeaderBytes);
   p.sp_ml = reinterpret_cast<float*>(ws + kHeaderBytes + split_pfx_bytes(batch));
-  p.sp_o = p.sp_ml + split_rows(G) * 2;
-  if (fp8) return launch_split<128, true>(p, batch, s);
-  switch (head_dim) {
-    case 64:
-      return launch_split<64, false>(p, batch, s);
-    case 80:
-      return launch_split<80, false>(p, batch, s);
-    case 96:
-      return launch_split<96, false>(p, batch, s);
-    default:
-      return launch_split<128, false>(p, batch, s);
+  p.sp_o = p.sp_ml + split_rows(G < kSplitMaxGroup ? G : kSplitMaxGroup) * 2;
+  p.q_group = G;
+  // query heads kSplitMaxGroup * c .. of every KV head group in launch c
+  for (int c0 = 0; c0 < G; c0 += kSplitMaxGroup) {
+    p.group = G - c0 < kSplitMaxGroup ? G - c0 : kSplitMaxGroup;
+    p.num_heads = num_kv_heads * p.group;
+    p.q = reinterpret_cast<const uint8_t*>(q) + (size_t)c0 * q_head_stride * sizeof(bf16_t);
+    p.out = reinterpret_cast<uint8_t*>(out) + (size_t)c0 * out_head_stride * sizeof(bf16_t);
+    int st;
+    if (fp8) {
+      st = launch_split<128, true>(p, batch, s);
+    } else {
+      switch (head_dim) {
+        case 64:
+          st = launch_split<64, false>(p, batch, s);
+          break;
+        case 80:
+          st = launch_split<80, false>(p, batch, s);
+          break;
+        case 96:
+          st = launch_split<96, false>(p, batch, s);
+          break;
+        default:
+          st = launch_split<128, false>(p, batch, s);
+      }
+    }
+    if (st != NIA_OK) return st;
   }
+  return NIA_OK;
 }
 
 }  // namespace

@@ -1027,7 +1027,10 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
     return launch_prefill_f32(f, true, head_dim, num_seqs, max_q_len, (hipStream_t)stream);
   }
   if (dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
-  if (block_size > 64 || (block_size & (block_size - 1))) return NIA_ERR_UNSUPPORTED;
+  // Power-of-two block sizes: a row's block and slot are a shift and a mask.  The key
+  // positions of a sequence (table width x block size) must fit an int.
+  if (block_size & (block_size - 1)) return NIA_ERR_UNSUPPORTED;
+  if ((int64_t)max_blocks_per_seq * block_size > INT32_MAX) return NIA_ERR_UNSUPPORTED;
   if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride) ||
       (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
     return NIA_ERR_MISALIGNED;

@@ -143,10 +143,13 @@ class Qwen3ForCausalLM(nn.Module):
 class KVPool:
     """Paged K/V caches of all layers plus a free list of their blocks.  With
     ``fp8`` the caches hold e4m3 codes (uint8) with one fp32 scale per
-    (block, KV head, slot) row in ``k_scale`` / ``v_scale``."""
+    (block, KV head, slot) row in ``k_scale`` / ``v_scale``.  The layout is checked
+    against every kernel the pool feeds when it is built (ops.check_pool_shape)."""
 
     def __init__(self, cfg: Qwen3Config, num_blocks: int, block_size: int, dtype, device,
                  fp8: bool = False):
+        ops.check_pool_shape(cfg.head_dim, block_size, cfg.num_heads, cfg.num_kv_heads,
+                             dtype, fp8)
         shape = (cfg.num_layers, num_blocks, cfg.num_kv_heads, block_size, cfg.head_dim)
         cdt = torch.uint8 if fp8 else dtype
         self.k_cache = torch.zeros(shape, dtype=cdt, device=device)

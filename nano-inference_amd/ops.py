@@ -200,18 +200,25 @@ def _dtype_code_of(dtype) -> int:
     return _DTYPES[dtype]
 
 
-def check_decode_shape(head_dim: int, block_size: int, num_heads: int, num_kv_heads: int,
-                       dtype=torch.bfloat16, fp8_cache: bool = False) -> None:
-    """Raise ValueError unless paged decode supports this layout (the limits of
-    include/nia_attn.h): bf16 - block size a power of two >= 4, head_dim 64 / 80 / 96 /
-    128, at most 16 query heads per KV head; fp8 caches - head_dim 128, block size a
-    power of two >= 16; fp32 - head_dim 64 / 80 / 96 / 128, any block size and group.
-    A KV pool can be checked when it is built, before any step runs."""
-    if num_kv_heads <= 0 or num_heads % num_kv_heads != 0:
+def check_pool_shape(head_dim: int, block_size: int, num_heads: int, num_kv_heads: int,
+                     dtype=torch.bfloat16, fp8_cache: bool = False) -> None:
+    """Raise ValueError unless every kernel a paged KV pool feeds supports its layout (the
+    limits of include/nia_attn.h), so that a pool can be checked when it is built, before
+    any step runs:
+
+    * bf16 caches: block size a power of two >= 4 (decode; chunked prefill takes any
+      power of two, the KV writes any size), head_dim 64 / 80 / 96 / 128, any group;
+    * fp8 caches: head_dim 128, block size a power of two >= 16;
+    * fp32 caches: head_dim 64 / 80 / 96 / 128, any block size and group.
+
+    Block sizes that are not powers of two are refused for bf16 and fp8 caches: the
+    kernels find a key's block and slot with a shift and a mask (the reference's block
+    size is a free integer, src/nano_inference/core/config.py:54; 16 is its default)."""
+    if num_kv_heads <= 0 or num_heads <= 0 or num_heads % num_kv_heads != 0:
         raise ValueError(f"num_heads must be divisible by num_kv_heads, got {num_heads=} and "
                          f"{num_kv_heads=}")
     if head_dim not in (64, 80, 96, 128):
-        raise ValueError(f"paged decode supports head_dim 64, 80, 96 or 128, not {head_dim}")
+        raise ValueError(f"paged attention supports head_dim 64, 80, 96 or 128, not {head_dim}")
     if block_size <= 0:
         raise ValueError(f"block_size must be positive, got {block_size}")
     if dtype == torch.float32 and not fp8_cache:
@@ -222,11 +229,15 @@ def check_decode_shape(head_dim: int, block_size: int, num_heads: int, num_kv_he
             raise ValueError("fp8 KV caches need head_dim 128 and a power-of-two block size "
                              f">= 16 (got head_dim {head_dim}, block_size {block_size})")
     elif not pow2 or block_size < 4:
-        raise ValueError("bf16 paged decode needs a power-of-two block size >= 4, "
+        raise ValueError("bf16 KV caches need a power-of-two block size >= 4, "
                          f"got {block_size}")
-    if num_heads // num_kv_heads > 16:
-        raise ValueError("bf16 paged decode takes at most 16 query heads per KV head, got "
-                         f"{num_heads // num_kv_heads}")
+
+
+def check_decode_shape(head_dim: int, block_size: int, num_heads: int, num_kv_heads: int,
+                       dtype=torch.bfloat16, fp8_cache: bool = False) -> None:
+    """Raise ValueError unless paged decode supports this layout: the same limits as
+    ``check_pool_shape`` (decode sets the pool's tightest ones)."""
+    check_pool_shape(head_dim, block_size, num_heads, num_kv_heads, dtype, fp8_cache)
 
 
 # One workspace per (device, stream): calls on one stream run one after another and may

@@ -250,12 +250,13 @@ class ChunkedCase:
 
 def chunked_qwen3_8b(device="cuda", dtype=torch.bfloat16, seed: int = 3103, n: int = 8,
                      chunk: int = 512, prior: Optional[List[int]] = None,
-                     num_heads: int = 32, num_kv_heads: int = 8) -> ChunkedCase:
+                     num_heads: int = 32, num_kv_heads: int = 8,
+                     block_size: int = 16) -> ChunkedCase:
     prior = uniform_lengths(n, 0, 8192, seed) if prior is None else list(prior)
-    bs = 16
+    bs = block_size
     ctx = [p + chunk for p in prior]
     nblk = [math.ceil(c / bs) for c in ctx]
-    pool = max(sum(nblk) + 64, 1024)
+    pool = max(sum(nblk) + 64, (1024 * 16) // bs)
     perm = torch.randperm(pool, generator=_gen(seed + 1, "cpu")).tolist()
     mb = max(nblk)
     tables = torch.zeros((n, mb), dtype=torch.int32)

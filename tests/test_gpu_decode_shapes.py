@@ -1,6 +1,7 @@
 """Paged decode over the layouts the reference's configuration allows: block sizes other
 than 16 (src/nano_inference/core/config.py:54 makes it a setting), head dims 64 / 80 / 96,
-groups up to 16, KV head counts whose groups of the split kernel take 1, 2 or 4 heads per
+any group (more than 16 query heads per KV head run as launches of at most 16 heads
+each), KV head counts whose groups of the split kernel take 1, 2 or 4 heads per
 workgroup, batches beyond the in-LDS unit prefix, and pools with invalid block ids.
 
 Oracle: oracle.textbook (softmax(q K^T / sqrt(D)) V over keys [0, context_len) gathered
@@ -90,6 +91,30 @@ def test_bf16_kv_head_counts_and_groups(hkv, group):
     assert_attn_close(out, oracle(c), torch.bfloat16, f"H_kv={hkv} G={group}")
 
 
+@pytest.mark.parametrize("hkv,group", [(1, 32), (2, 20), (1, 17), (4, 48)])
+def test_bf16_groups_beyond_16(hkv, group):
+    """More than 16 query heads per KV head (multi-query attention and wide GQA): the
+    reference repeats each KV head G times (src/nano_inference/layers/attention.py:
+    310-314), any G; here the heads run 16 at a time over the same keys.  One empty
+    context and a batch of 1100 (unit prefix in the workspace) for one of them."""
+    lens = [5, 77, 1000, 2047, 33, 0, 300]
+    c = workloads.make_decode(len(lens), hkv * group, hkv, 128, [max(L, 1) for L in lens], 512,
+                              16, torch.bfloat16, "cuda", seed=1240 + 17 * hkv + group)
+    ops.kv_write(c.k_new, c.v_new, c.k_cache[0], c.v_cache[0], c.slot_mapping)
+    ctx = torch.tensor(lens, dtype=torch.int64, device="cuda")
+    out = ops.paged_decode(c.q, c.k_cache[0], c.v_cache[0], c.block_tables, ctx)
+    torch.cuda.synchronize()
+    assert out[5].eq(0).all()
+    c.lens = lens
+    assert_attn_close(out, oracle(c), torch.bfloat16, f"H_kv={hkv} G={group}")
+    if group == 20:
+        lens = [int(x) for x in torch.randint(1, 41, (1100,),
+                                              generator=torch.Generator().manual_seed(5))]
+        c = workloads.make_decode(1100, hkv * group, hkv, 128, lens, 4096, 16, torch.bfloat16,
+                                  "cuda", seed=1250, max_blocks=4)
+        assert_attn_close(step(c), oracle(c), torch.bfloat16, f"G={group} batch 1100")
+
+
 @pytest.mark.parametrize("batch", [1, 3])
 def test_bf16_one_long_sequence_over_many_ranges(batch):
     """A 64k-token context cut over every wave of the grid (combine of hundreds of
@@ -172,6 +197,5 @@ def test_unsupported_layouts_raise_before_launch():
     c = workloads.make_decode(2, 8, 2, 128, [5, 9], 8, 2, torch.bfloat16, "cuda", seed=1280)
     with pytest.raises(ValueError, match="block size"):
         ops.paged_decode(c.q, c.k_cache[0], c.v_cache[0], c.block_tables, c.context_lens)
-    with pytest.raises(ValueError, match="16 query heads"):
-        ops.check_decode_shape(128, 16, 32, 1)
+    ops.check_decode_shape(128, 16, 32, 1)  # any group
     ops.check_decode_shape(128, 2, 32, 1, torch.float32)  # fp32 takes any layout

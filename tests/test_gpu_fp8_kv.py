@@ -140,7 +140,7 @@ def test_decode_fp8_small():
     assert_attn_close(run_fp8(c, f8), oracle_decode_fp8(c, f8), torch.bfloat16, "fp8 small")
 
 
-@pytest.mark.parametrize("g", [1, 2, 4, 7, 8])
+@pytest.mark.parametrize("g", [1, 2, 4, 7, 8, 16, 24, 32])
 def test_decode_fp8_group_sizes(g):
     lens = [1, 15, 16, 17, 300, 513, 1100]
     c = workloads.make_decode(len(lens), 2 * g, 2, 128, lens, 256, 16, torch.bfloat16, "cuda",
@@ -152,9 +152,9 @@ def test_decode_fp8_group_sizes(g):
 @pytest.mark.parametrize("batch", [1024, 1025])
 @pytest.mark.parametrize("heads", [16, 28])
 def test_decode_fp8_at_the_staged_batch_limit(heads, batch):
-    """fp8 batches of up to 1024 sequences run the matrix-core loop (codes staged through
-    LDS); above it groups of 4 take the vector loop at three workgroups per CU and groups
-    of 7 the plain vector loop.  Short contexts (1 to 40 tokens) keep the oracle quick."""
+    """fp8 batches of up to 1024 sequences build the split kernel's unit prefix in LDS;
+    above it decode_prefix_kernel writes it to the workspace first.  Groups of 4 and 7,
+    short contexts (1 to 40 tokens) keep the oracle quick."""
     lens = [int(x) for x in torch.randint(1, 41, (batch,),
                                           generator=torch.Generator().manual_seed(batch + 7))]
     c = workloads.make_decode(batch, heads, 4, 128, lens, 4096, 16, torch.bfloat16, "cuda",

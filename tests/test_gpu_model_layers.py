@@ -160,8 +160,12 @@ class PackedStepper:
         return out, exp
 
 
+@pytest.mark.parametrize("bs", [16, 128, 256])
 @pytest.mark.parametrize("fp8", [False, True])
-def test_packed_step_qwen3_0p6b_layer(fp8):
+def test_packed_step_qwen3_0p6b_layer(fp8, bs):
+    """Three packed steps (prefill chunks, then decodes mixed with chunks, then decodes),
+    block sizes 16, 128 and 256: with the larger blocks most chunks and decode rows sit
+    inside one block and some cross into the next."""
     torch.manual_seed(10)
     m = PagedCausalSelfAttention(1024, 16, num_kv_heads=8, head_dim=128, use_qk_norm=True,
                                  rope_base=1e6).to("cuda", torch.bfloat16).eval()
@@ -169,7 +173,7 @@ def test_packed_step_qwen3_0p6b_layer(fp8):
         m.q_norm.weight.copy_(1 + 0.3 * torch.randn(128))
         m.k_norm.weight.copy_(1 + 0.3 * torch.randn(128))
     m.layer_idx = 0
-    bs, nb = 16, 256
+    nb = 4096 // bs
     st = PackedStepper(m, nb, bs, fp8)
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(11)).tolist()
     prompts = [40, 300, 17, 150, 90, 260]
@@ -182,18 +186,18 @@ def test_packed_step_qwen3_0p6b_layer(fp8):
     e1 = [(0, 40, False), (0, 300, False), (0, 17, False), (0, 64, False), (0, 1, False),
           (0, 100, False)]
     out, exp = st.step(e1, tables, 1)
-    close(out, exp, f"packed prefill chunks fp8={fp8}")
+    close(out, exp, f"packed prefill chunks fp8={fp8} bs={bs}")
     # step 2: three decodes plus the others' next chunks, ending prompt 4 and 5
     e2 = [(40, 1, True), (300, 1, True), (17, 1, True), (64, 86, False), (1, 89, False),
           (100, 60, False)]
     out, exp = st.step(e2, tables, 2)
-    close(out[0, :3], exp[0, :3], f"packed step decode rows fp8={fp8}")
-    close(out, exp, f"packed step mixed fp8={fp8}")
+    close(out[0, :3], exp[0, :3], f"packed step decode rows fp8={fp8} bs={bs}")
+    close(out, exp, f"packed step mixed fp8={fp8} bs={bs}")
     # step 3: all six decode, one more chunk for the last prompt first
     e3 = [(41, 1, True), (301, 1, True), (18, 1, True), (150, 1, True), (90, 1, True),
           (160, 100, False)]
     out, exp = st.step(e3, tables, 3)
-    close(out, exp, f"packed step 3 fp8={fp8}")
+    close(out, exp, f"packed step 3 fp8={fp8} bs={bs}")
 
 
 def _vl_mrope_prompt(text_before, grid_h, grid_w, text_after):
