@@ -15,7 +15,10 @@ reference pipeline restated in float64 on the CPU.
   343-371 and :220-340); metadata from the oracle's restated context builder.
 * Teacher forcing on a 2-layer Qwen3-0.6B-architecture model (full vocabulary):
   every greedy token of both generators must be a maximum of the float64 CPU
-  recompute's logits at its position, up to bf16 noise.
+  recompute's logits at its position, up to bf16 noise; at the end-to-end workload's
+  own scheduling (prompts of 1000-2048 tokens, 1024-token chunks, 8192-token steps,
+  graph-replayed decode steps, bf16 and fp8 pools) each token must be the float64
+  argmax unless the top-2 margin is below a measured bf16-noise bound.
 Module-level bar (bf16 activations between every op on the GPU side):
 max-abs <= 3e-2, mean-abs <= 3e-3.
 """
@@ -348,3 +351,79 @@ def test_generation_qwen3_0p6b_shape_matches_float64_model(mixed):
     st = gen.run(prompts)
     assert st.generated_tokens == len(prompts) * new
     _teacher_forcing(gen, prompts, new)
+
+
+# ---- teacher forcing at the Qwen3-0.6B workload's own scheduling -----------------------
+
+_CPU_LOGITS: dict = {}
+
+
+def _gpu_dense_logits(model, seq, rows):
+    """The GPU model's own logits at ``rows`` of ``seq``, one dense causal forward (no
+    cache): the bf16 noise of the model against the float64 recompute."""
+    ids = torch.tensor(seq, device="cuda").view(1, -1)
+    pos = torch.arange(len(seq), device="cuda").view(1, -1)
+    with torch.no_grad():
+        x = model.embed_tokens(ids)
+        for layer in model.layers:
+            x = layer(x, pos, None, None)
+        return model.lm_head(model.norm(x[0, rows])).double().cpu()
+
+
+def _teacher_forcing_argmax(gen, prompts, new, what, model_tag):
+    """Every greedy token must be the float64 recompute's argmax at its position, unless
+    the float64 top-2 margin there is below the bf16-noise bound; then the token must lie
+    within that bound of the maximum.  The bound is twice the largest |logit| difference
+    between the GPU model's dense bf16 forward and the float64 recompute over the same
+    positions (two logits, each off by at most that much, decide a comparison); that
+    noise itself must stay under 2 % of the logit scale."""
+    cpu = None
+    exact = near = 0
+    for prompt, out in zip(prompts, gen.outputs):
+        assert len(out) == new
+        seq = list(prompt) + list(out[:-1])
+        rows = list(range(len(prompt) - 1, len(seq)))
+        key = (model_tag, tuple(seq))  # same weights (same seed): same float64 logits
+        if key not in _CPU_LOGITS:
+            cpu = cpu or CpuQwen3(gen.model)
+            _CPU_LOGITS[key] = cpu.logits(seq, rows)
+        lg = _CPU_LOGITS[key]
+        gl = _gpu_dense_logits(gen.model, seq, rows)
+        scale = lg.abs().max().item()
+        noise = (gl - lg).abs().max().item()
+        assert noise <= 2e-2 * scale, f"{what}: bf16 logit noise {noise:.3g} of scale {scale:.3g}"
+        bound = 2 * noise
+        for i, tok in enumerate(out):
+            row = lg[i]
+            top2 = torch.topk(row, 2)
+            best, margin = int(top2.indices[0]), (top2.values[0] - top2.values[1]).item()
+            if tok == best:
+                exact += 1
+                continue
+            gap = (top2.values[0] - row[tok]).item()
+            assert margin < bound and gap <= bound, (
+                f"{what} position {i}: chose {tok}, float64 argmax {best} (margin {margin:.3g}, "
+                f"gap {gap:.3g}, noise bound {bound:.3g})")
+            near += 1
+    print(f"TEACHER {what}: {exact} float64 argmax, {near} within the noise bound", flush=True)
+
+
+@pytest.mark.parametrize("mode", ["prefill_first", "mixed", "mixed_fp8"])
+def test_generation_at_the_qwen3_0p6b_workload_scheduling(mode):
+    """The end-to-end workload's scheduling parameters on a 2-layer Qwen3-0.6B-shaped model
+    (full vocabulary): 8 prompts of U[1000, 2048] random ids, 8 greedy tokens each; the
+    prefill-first generator with padded prefill batches of 8 and graph-replayed decode
+    steps, or the mixed generator with 1024-token chunks in steps of up to 8192 tokens
+    (decodes mixed with the later chunks) and the graph-replayed all-decode tail, over a
+    bf16 or an fp8 KV pool.  Checked by teacher forcing against the float64 model."""
+    cfg = _qwen3_0p6b_two_layers()
+    prompts = e2e.generation_prompts(8, 1000, 2048, cfg.vocab_size, seed=43)
+    new = 8
+    gen = e2e.build(cfg, prompts, max_new_tokens=new, max_prefill_batch=8, seed=9,
+                    mixed=mode != "prefill_first", max_step_tokens=8192, chunk=1024,
+                    use_graph=True, fp8_cache=mode == "mixed_fp8")
+    st = gen.run(prompts)
+    assert st.generated_tokens == len(prompts) * new
+    if mode != "prefill_first":
+        assert st.prefill_steps >= 2  # the prompts (~12k tokens) need more than one step
+    _teacher_forcing_argmax(gen, prompts, new, mode, "qwen3-0.6b-2-layers-seed-9")
