@@ -110,6 +110,20 @@ NIA_DEVICE bool prefill_map(const PrefillParams& p, int& seq, int& h, int& mb) {
   return true;
 }
 
+// Paired-head grids (one query head per KV head, short unmasked sequences): all head pairs
+// of a sequence on one XCD (sequence % 8), so the cache lines that two neighbouring pairs'
+// rows share (a D = 80 row is 160 bytes) are fetched into one L2 once.
+NIA_DEVICE bool pair_map(const PrefillParams& p, int& seq, int& h, int& mb) {
+  const int id = blockIdx.x;
+  const int x = id % kXcds;
+  const int t = id / kXcds;
+  const int j = t / p.num_kv_heads;
+  seq = x + kXcds * j;
+  h = t - j * p.num_kv_heads;
+  mb = 0;
+  return seq < p.num_seqs;
+}
+
 // Rank-major variant, for grids whose workgroups of one sequence all do about the same
 // work (non-causal calls, and chunks after a cached context): sequences are ranked by
 // key length (longest first), the groups of rank r go out before those of rank r + 1
@@ -489,6 +503,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
+  // D % 32 == 16 (D = 80): the last P.V tile's 16 padded dims D .. D + 15 carry the row
+  // sums instead of the vector unit.  Those V columns are never written by the DMA; they
+  // hold 1.0 at dim D and zeros, so O^T row D accumulates sum_k P[k] with O's own
+  // rescales, and the lazy check tests the largest exponent instead of a lane sum.
+  constexpr bool kSumRow = D % 32 == 16;
   // One array per stage and operand: the compiler then sees that the DMA into one stage
   // cannot alias the LDS reads of the other and issues no vmcnt wait before those reads
   // (with one [stage][K, V] array it waited for the next tile's DMA inside every tile).
@@ -501,7 +520,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
 
   int seq, h, mb;
   if constexpr (PAIR) {
-    if (!prefill_map(p, seq, h, mb)) return;
+    if (!pair_map(p, seq, h, mb)) return;
   } else {
     if (!map_workgroup<PAGED>(p, seq, h, mb)) return;
   }
@@ -512,6 +531,16 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   const int col = lane & 31;
   if constexpr (PAIR) h = 2 * h + (wave >> 1);  // the map numbers head pairs
   const int wrow = PAIR ? (wave & 1) : wave;    // 32-row group of the m-block
+  if constexpr (kSumRow) {
+    // V rows of both buffers: chunk D / 8 = (1.0, 0, ..., 0), chunk D / 8 + 1 = 0, at their
+    // swizzled positions (one 16-byte store per thread)
+    const int r = tid & 63;
+    const int c = kChunks + ((tid >> 7) & 1);
+    uint8_t* vtile = (tid >> 6) & 1 ? lds_v1 : lds_v0;
+    const uint32_t one = c == kChunks ? 0x3F80u : 0u;  // bf16 1.0 in the low half
+    *reinterpret_cast<uint4*>(vtile + r * kTileRowBytes + 16 * (c ^ tile_swz(r))) =
+        make_uint4(one, 0u, 0u, 0u);
+  }
 
   const int qlen = p.q_len[seq];
   const int m0 = mb * (PAIR ? kBlockM / 2 : kBlockM);
@@ -692,6 +721,51 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         for (int r = 0; r < 16; ++r)
           if (32 * c + 8 * (r >> 2) + (r & 3) >= lim) sacc[c][r] = -INFINITY;
     }
+    if constexpr (kSumRow) {
+      // The row sums come from the matrix cores, so the lazy check needs no sum of P: the
+      // lane's largest raw score (v_max3 over its 32) is tested against the running max
+      // before any exponential, the max raised and O rescaled only when a P could exceed
+      // 2^8 (or the row has no max yet).  Then P and P.V go chunk by chunk (16 keys) with
+      // no branch between them, so chunk kc's products run on the matrix cores while the
+      // vector unit computes chunk kc + 1's P.
+      float smax = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) smax = fmaxf(smax, sacc[c][r]);
+      if (wave_any(!(fmaf(smax, p.scale_log2, -m_run) <= kLazyRescaleP))) {
+        const float mn = fmaxf(m_run, max_xor32(smax) * p.scale_log2);
+        const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
+        m_run = mn;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= corr;
+      }
+      const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const int c = kc >> 1, hh = kc & 1;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float x0 = fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub);
+          const float x1 = fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub);
+          w[j] = pack_bf16x2(fast_exp2(x0), fast_exp2(x1));
+        }
+        const uint4 pbk = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const s16x4_t lo = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off[dt]);
+          const s16x4_t hi = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off2[dt]);
+          const s16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, pbk), oacc[dt], 0,
+              0, 0);
+        }
+      }
+      return;  // the rest of the tile is the lane-sum form of the other head dims
+    }
     // P against the running max: p = exp2(s * scale * log2(e) - m), one FMA per score in
     // fp32 (scaling Q in bf16 instead would round every score by up to 2^-9 of its size,
     // which at logits of tens of nats moves the weights by percents).  The tile's max is
@@ -801,8 +875,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   }
 
   // ---- epilogue --------------------------------------------------------------------------
+  // the row sum: lanes l and l ^ 32 each hold half of it, or (kSumRow) O^T row D, which
+  // lane l % 32 holds in register 8 of the last tile
+  const float lt = kSumRow ? __shfl(oacc[DT - 1][8], col, kWave)
+                           : l_run + __shfl_xor(l_run, 32, kWave);
   if (!row_ok) return;
-  const float lt = l_run + __shfl_xor(l_run, 32, kWave);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   bf16_t* op = p.o + (qstart + qrow) * p.o_tok + (int64_t)h * p.o_head;
 #pragma unroll
@@ -952,7 +1029,7 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
     p.num_kv_heads = num_kv_heads / 2;  // the workgroup map numbers head pairs
     p.groups_per_xcd = (num_seqs * p.num_kv_heads + kXcds - 1) / kXcds;
     p.num_m_blocks = 1;
-    const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd;
+    const int64_t nwg = (int64_t)kXcds * ((num_seqs + kXcds - 1) / kXcds) * p.num_kv_heads;
     if (nwg >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
     switch (head_dim) {

@@ -1,4 +1,7 @@
-"""End-to-end generation over the paged path vs a dense recompute of the same tokens.
+"""End-to-end generation over the paged path vs a dense recompute of the same tokens by
+the same model: a self-consistency check of the generators' bookkeeping (slots, tables,
+positions, chunk boundaries, graph replays).  The comparison with an independent float64
+model is tests/test_gpu_model_layers.py's teacher forcing.
 
 Both generators are checked: prefill-first (padded prefill batches, then a graph
 decode step) and mixed (chunked prefill and decodes packed into the same steps).
