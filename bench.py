@@ -534,7 +534,9 @@ def profile_run(torch, ops, workloads, name: str, n: int) -> None:
         out = torch.empty_like(c.q)
         for _ in range(n):
             ops.prefill(c.q, c.k, c.v, qs, ql, qs, ql, max(c.lens), mode, out=out)
-        info = dict(flops=c.flops(), algorithmic_bytes=4 * c.q.numel() * c.q.element_size())
+        # q read and o written once, k and v read once
+        info = dict(flops=c.flops(),
+                    algorithmic_bytes=(2 * c.q.numel() + 2 * c.k.numel()) * c.q.element_size())
     else:
         raise SystemExit(f"bench.py: unknown profile workload {name!r}; one of "
                          f"{', '.join(PROFILE_WORKLOADS)}")
