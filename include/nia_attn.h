@@ -53,7 +53,7 @@ extern "C" {
 #define NIA_ERR_MISALIGNED 5       /* a pointer or stride breaks 16-byte vector access */
 #define NIA_ERR_SCRATCH_LIMIT 6    /* the call needs more than the library's fixed scratch */
 
-/* Library ABI version; bumped whenever a signature below changes. */
+/* Library ABI version; bumped whenever a signature below changes or an entry point is added. */
 int32_t nia_abi_version(void);
 
 /* Human-readable name of a status code (static storage, never NULL). */
@@ -169,6 +169,32 @@ int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
                     int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
                     int32_t num_kv_heads, int32_t head_dim, float scale, int32_t causal,
                     int32_t dtype, void* stream);
+
+/*
+ * nia_prefill with an additive mask of any shape.  Replaces the general form of the
+ * reference's mask at src/nano_inference/layers/attention.py:40-47, which adds any
+ * broadcastable attention_mask (sliced to S_k) to the scaled scores before the fp32
+ * softmax; nia_prefill covers the prefix masks the reference's own callers build
+ * (context_builder.py:141-149 through :321-326) by key lengths.  mask is fp32, 16-byte
+ * aligned; the value added to the scaled score of query row i (within its sequence) and
+ * key j of sequence s and query head h is
+ *     mask[s * mask_seq_stride + h * mask_head_stride + i * mask_q_stride + j]
+ * (element strides, multiples of 4 and >= 0; 0 broadcasts), read for keys j < k_len[s]
+ * and rows i < q_len[s] only.  -inf masks a key; the causal mode still applies.  A row
+ * whose every key is masked produces zeros (the reference's softmax gives NaN there).
+ * Same support as nia_prefill, except that bf16 K/V token strides must stay below 2^26
+ * elements (else NIA_ERR_UNSUPPORTED); mask == NULL returns NIA_ERR_INVALID_ARGUMENT.
+ */
+int32_t nia_prefill_masked(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                           const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                           const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                           const int32_t* q_start, const int32_t* q_len,
+                           const int32_t* k_start, const int32_t* k_len,
+                           int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, float scale, int32_t causal,
+                           int32_t dtype, const float* mask, int64_t mask_seq_stride,
+                           int64_t mask_head_stride, int64_t mask_q_stride, void* stream);
 
 /*
  * Chunked prefill over the paged KV cache.  Has no counterpart in the

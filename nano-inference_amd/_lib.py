@@ -71,6 +71,12 @@ SIGNATURES = {
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64,
          _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p],
     ),
+    "nia_prefill_masked": (
+        _i32,
+        [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64,
+         _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _i32,
+         _p, _i64, _i64, _i64, _p],
+    ),
     "nia_prefill_paged": (
         _i32,
         [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i32, _i32, _p, _p, _p,
@@ -107,7 +113,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # The entry points _nia_fast wraps: one call per layer and step.
 FAST_CALLS = (

@@ -20,9 +20,12 @@ from the reference, all where the reference has no defined behaviour of its own:
   sequence attends with a bottom-right causal mask (chunked prefill); the
   reference applies no causal mask when S_q != S_k
   (src/nano_inference/layers/attention.py:33-38);
-* a padding mask must be a prefix mask (keys [0, len) visible), which is what
-  the context builder produces (src/nano_inference/engine/context_builder.py:
-  141-149); other masks raise NotImplementedError.
+* a query row whose every key is masked gives zeros (the reference's softmax gives
+  NaN).
+Masks: a prefix (right-padding) mask, which is what the context builder produces
+(src/nano_inference/engine/context_builder.py:141-149), becomes per-sequence key
+lengths; any other mask is added to the scaled scores as the reference adds it
+(src/nano_inference/layers/attention.py:40-47) by nia_prefill_masked.
 """
 from __future__ import annotations
 
@@ -40,11 +43,11 @@ _PREFIX = ops.TensorMemo()
 
 
 def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int,
-                    device: torch.device) -> torch.Tensor:
-    """Visible-key counts (int32, on ``device``) of a prefix mask; raises for any other
-    mask shape.
+                    device: torch.device) -> Optional[torch.Tensor]:
+    """Visible-key counts (int32, on ``device``) of a prefix mask, or None when the mask
+    is not one (the general additive path then takes it).
 
-    Accepts the reference's two mask forms: 2-D bool (B, S_total) with True =
+    Prefix masks come in the reference's two forms: 2-D bool (B, S_total) with True =
     visible, or additive (B, 1, 1, S_total) with 0 = visible and -inf = masked.
     Checking that the mask is a prefix reads it back to the host; the result is kept
     per mask tensor (ops.TensorMemo), so the layers of a step that share one mask pay
@@ -53,22 +56,53 @@ def _prefix_lengths(mask: torch.Tensor, batch: int, key_len: int,
     key = (batch, key_len, device)
     lens = _PREFIX.get(mask, key)
     if lens is not None:
-        return lens
-    if mask.dim() == 2:
+        return None if isinstance(lens, bool) else lens
+    lens = False
+    if mask.dim() == 2 and mask.shape[0] in (1, batch):
         vis = mask[:, :key_len].to(torch.bool)
-    elif mask.dim() == 4 and mask.shape[1] == 1 and mask.shape[2] == 1:
-        vis = mask[:, 0, 0, :key_len] == 0
+    elif (mask.dim() == 4 and mask.shape[0] in (1, batch) and mask.shape[1] == 1
+          and mask.shape[2] == 1):
+        m = mask[:, 0, 0, :key_len]
+        vis = m == 0
+        if not torch.all(vis | (m == float("-inf"))):
+            vis = None  # finite non-zero values: not a pure visibility mask
     else:
-        raise NotImplementedError(f"attention_mask of shape {tuple(mask.shape)}")
-    if vis.shape[0] != batch:
-        vis = vis.expand(batch, -1)
-    n = vis.sum(dim=-1)
-    ar = torch.arange(vis.shape[-1], device=vis.device)
-    if not torch.equal(vis, ar.unsqueeze(0) < n.unsqueeze(1)):
-        raise NotImplementedError("only prefix (right-padding) attention masks are supported")
-    lens = n.to(device=device, dtype=torch.int32)
+        vis = None
+    if vis is not None and vis.shape[-1] == key_len:
+        if vis.shape[0] != batch:
+            vis = vis.expand(batch, -1)
+        n = vis.sum(dim=-1)
+        ar = torch.arange(vis.shape[-1], device=vis.device)
+        if torch.equal(vis, ar.unsqueeze(0) < n.unsqueeze(1)):
+            lens = n.to(device=device, dtype=torch.int32)
     _PREFIX.put(mask, key, lens)
-    return lens
+    return None if lens is False else lens
+
+
+def _additive_mask(mask: torch.Tensor, b: int, h: int, sq: int, sk: int,
+                   dtype: torch.dtype) -> torch.Tensor:
+    """The mask the reference adds to the (B, H, S_q, S_k) scores (src/nano_inference/
+    layers/attention.py:40-47): sliced to S_k and cast to the scores' dtype, as a 4-D
+    tensor that broadcasts against (B, H, S_q, S_k).  A 2-D bool (B, S) mask is the
+    layers' visibility form (:321-326): True visible, False -inf."""
+    if mask.shape[-1] > sk:
+        mask = mask[..., :sk]
+    if mask.dim() == 2 and mask.dtype == torch.bool:
+        add = torch.zeros(mask.shape, dtype=dtype, device=mask.device)
+        add = add.masked_fill(~mask, float("-inf"))
+        mask = add.view(mask.shape[0], 1, 1, -1)
+    else:
+        mask = mask.to(dtype)
+    while mask.dim() < 4:
+        mask = mask.unsqueeze(0)
+    try:
+        torch.broadcast_shapes(mask.shape, (b, h, sq, sk))
+    except RuntimeError:
+        raise ValueError(f"attention_mask of shape {tuple(mask.shape)} does not broadcast "
+                         f"to the scores ({b}, {h}, {sq}, {sk})") from None
+    if mask.shape[-1] != sk:
+        mask = mask.expand(*mask.shape[:3], sk)
+    return mask
 
 
 _INDEX_CACHE: dict = {}
@@ -139,9 +173,14 @@ def scaled_dot_product_attention(
         out = torch.empty(b, sq, h, d, dtype=q.dtype, device=dev).transpose(1, 2)
         o3, q_step, k_step = out.transpose(1, 2).view(b * sq, h, d), sq, sk
     q_start, q_len, k_start, k_len = _seq_index(b, q_step, sq, k_step, sk, dev)
+    bias = None
     if attention_mask is not None:
-        k_len = _prefix_lengths(attention_mask, b, sk, dev)
-    ops.prefill(q3, k3, v3, q_start, q_len, k_start, k_len, sq, causal, out=o3)
+        lens = _prefix_lengths(attention_mask, b, sk, dev)
+        if lens is not None:
+            k_len = lens
+        else:
+            bias = _additive_mask(attention_mask, b, h, sq, sk, q.dtype)
+    ops.prefill(q3, k3, v3, q_start, q_len, k_start, k_len, sq, causal, out=o3, mask=bias)
     return out
 
 
@@ -243,13 +282,18 @@ class PagedCausalSelfAttention(CausalSelfAttentionBase):
         b, s = q.shape[:2]
         dev = q.device
         ar, lens, _, k_len = _seq_index(b, s, s, s, s, dev)
+        bias = None
         if attention_mask is not None:
-            k_len = _prefix_lengths(attention_mask, b, s, dev)
+            plen = _prefix_lengths(attention_mask, b, s, dev)
+            if plen is not None:
+                k_len = plen
+            else:
+                bias = _additive_mask(attention_mask, b, self.num_heads, s, s, q.dtype)
         return ops.prefill(
             q.reshape(b * s, self.num_heads, self.head_dim),
             k.reshape(b * s, self.num_kv_heads, self.head_dim),
             v.reshape(b * s, self.num_kv_heads, self.head_dim),
-            ar, lens, ar, k_len, s, ops.CAUSAL_TOP_LEFT,
+            ar, lens, ar, k_len, s, ops.CAUSAL_TOP_LEFT, mask=bias,
         )
 
     def forward(

@@ -1,7 +1,7 @@
 // Library-wide entry points of the C ABI: version and status names.
 #include "common.h"
 
-extern "C" int32_t nia_abi_version(void) { return 2; }
+extern "C" int32_t nia_abi_version(void) { return 3; }
 
 extern "C" const char* nia_error_string(int32_t status) {
   switch (status) {

@@ -79,6 +79,11 @@ struct PrefillParams {
   int32_t order_by_len;    // rank-major grid over sequences sorted by key length
   int32_t causal;
   float scale_log2;
+  // additive mask (nia_prefill_masked): bias[s * bias_seq + h * bias_head + i * bias_q + j]
+  // is added to the scaled score of query row i and key j of sequence s, head h
+  const float* bias;
+  int64_t bias_seq, bias_head, bias_q;
+  float scale;
 };
 
 // Workgroup -> (sequence, head, m-block) mapping of the 1-D prefill grid.
@@ -496,10 +501,13 @@ constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
 // waves 0-1 the 64 rows of the first and waves 2-3 those of the second, each pair of
 // waves with its own K/V buffer (the two stages), single-buffered.  Half as many
 // workgroups, none of them with idle waves.
-template <int D, bool PAGED, bool PAIR = false>
+// BIAS (contiguous K/V, no pairing): an additive fp32 mask joins the scaled scores, which
+// are then carried in nats (exponent scale log2 e instead of scale * log2 e).
+template <int D, bool PAGED, bool PAIR = false, bool BIAS = false>
 __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(PrefillParams p) {
   static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
   static_assert(!(PAIR && PAGED), "paired heads read contiguous K/V");
+  static_assert(!(BIAS && (PAIR || PAGED)), "masks apply to contiguous, unpaired calls");
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
@@ -689,6 +697,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         (vr15 + 8) * kTileRowBytes + 16 * ((4 * dt + vcd) ^ tile_swz(vr15 + 8)) + 8 * (i16 & 1);
   }
 
+  // the exponent scale of the scores as the tile carries them
+  const float sl = BIAS ? kLog2e : p.scale_log2;
+  const float* bias_row = nullptr;  // BIAS: this lane's query row of the mask
+  if constexpr (BIAS)
+    bias_row = p.bias + (int64_t)seq * p.bias_seq + (int64_t)h * p.bias_head +
+               (int64_t)(row_ok ? qrow : 0) * p.bias_q;
   auto compute_tile = [&](int n0, int stage) __attribute__((always_inline)) {
     const uint8_t* kt = tile_k(stage);
     const uint8_t* vt = tile_v(stage);
@@ -721,6 +735,35 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         for (int r = 0; r < 16; ++r)
           if (32 * c + 8 * (r >> 2) + (r & 3) >= lim) sacc[c][r] = -INFINITY;
     }
+    if constexpr (BIAS) {
+      // scores in nats: scale * q . k + mask; keys n0 + 4 half + 32 c + 8 g .. + 3 of this
+      // lane's query (past the context they are -inf already and the mask is not read)
+      if (row_ok) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int key = n0 + 4 * half + 32 * c + 8 * g;
+            float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (key + 3 < klen) {
+              bv = *reinterpret_cast<const float4*>(bias_row + key);
+            } else if (key < klen) {
+              bv.x = bias_row[key];
+              if (key + 1 < klen) bv.y = bias_row[key + 1];
+              if (key + 2 < klen) bv.z = bias_row[key + 2];
+            }
+            sacc[c][4 * g + 0] = fmaf(sacc[c][4 * g + 0], p.scale, bv.x);
+            sacc[c][4 * g + 1] = fmaf(sacc[c][4 * g + 1], p.scale, bv.y);
+            sacc[c][4 * g + 2] = fmaf(sacc[c][4 * g + 2], p.scale, bv.z);
+            sacc[c][4 * g + 3] = fmaf(sacc[c][4 * g + 3], p.scale, bv.w);
+          }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[c][r] *= p.scale;
+      }
+    }
     if constexpr (kSumRow) {
       // The row sums come from the matrix cores, so the lazy check needs no sum of P: the
       // lane's largest raw score (v_max3 over its 32) is tested against the running max
@@ -733,8 +776,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) smax = fmaxf(smax, sacc[c][r]);
-      if (wave_any(!(fmaf(smax, p.scale_log2, -m_run) <= kLazyRescaleP))) {
-        const float mn = fmaxf(m_run, max_xor32(smax) * p.scale_log2);
+      if (wave_any(!(fmaf(smax, sl, -m_run) <= kLazyRescaleP))) {
+        const float mn = fmaxf(m_run, max_xor32(smax) * sl);
         const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
         m_run = mn;
 #pragma unroll
@@ -749,8 +792,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float x0 = fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, -msub);
-          const float x1 = fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, -msub);
+          const float x0 = fmaf(sacc[c][8 * hh + 2 * j], sl, -msub);
+          const float x1 = fmaf(sacc[c][8 * hh + 2 * j + 1], sl, -msub);
           w[j] = pack_bf16x2(fast_exp2(x0), fast_exp2(x1));
         }
         const uint4 pbk = make_uint4(w[0], w[1], w[2], w[3]);
@@ -783,8 +826,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
           uint32_t w[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float x0 = fmaf(sacc[c][8 * hh + 2 * j], p.scale_log2, shift);
-            const float x1 = fmaf(sacc[c][8 * hh + 2 * j + 1], p.scale_log2, shift);
+            const float x0 = fmaf(sacc[c][8 * hh + 2 * j], sl, shift);
+            const float x1 = fmaf(sacc[c][8 * hh + 2 * j + 1], sl, shift);
             w[j] = pack_bf16x2(fast_exp2(x0), fast_exp2(x1));
             lt = dot2_bf16(w[j], kBf16OnePair, lt);
           }
@@ -803,7 +846,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[c][r]);
-      const float mn = fmaxf(m_run, max_xor32(mx) * p.scale_log2);
+      const float mn = fmaxf(m_run, max_xor32(mx) * sl);
       const float corr = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - mn);
       m_run = mn;
       const float msub_new = (mn == -INFINITY) ? 0.f : mn;
@@ -899,7 +942,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
 
 constexpr int64_t kMaxRowStride = (int64_t)1 << 26;  // elements
 
-template <bool PAGED>
+template <bool PAGED, bool BIAS = false>
 int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream_t s) {
   const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd * p.group * p.num_m_blocks;
   if (nwg >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
@@ -909,10 +952,14 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
   const bool dma_ok = PAGED ? p.bs_log2 >= 4
                             : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
                                p.v_tok < kMaxRowStride);
+  if (BIAS && !dma_ok) return NIA_ERR_UNSUPPORTED;
   switch (head_dim) {
 #define NIA_PREFILL_CASE(DD)                                                                 \
   case DD:                                                                                   \
-    if (dma_ok)                                                                              \
+    if (BIAS)                                                                                \
+      nia_launch((prefill_dma_kernel<DD, false, false, true>), grid, dim3(kPrefillThreads),  \
+                 s, p);                                                                      \
+    else if (dma_ok)                                                                         \
       nia_launch((prefill_dma_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), s, p);        \
     else                                                                                     \
       nia_launch((prefill_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), s, p);            \
@@ -941,15 +988,17 @@ bool vec_ok_f32(const void* ptr, int64_t a, int64_t b) {
 
 }  // namespace
 
-extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
-                               const void* q, int64_t q_tok_stride, int64_t q_head_stride,
-                               const void* k, int64_t k_tok_stride, int64_t k_head_stride,
-                               const void* v, int64_t v_tok_stride, int64_t v_head_stride,
-                               const int32_t* q_start, const int32_t* q_len,
-                               const int32_t* k_start, const int32_t* k_len, int32_t num_seqs,
-                               int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
-                               int32_t head_dim, float scale, int32_t causal, int32_t dtype,
-                               void* stream) {
+namespace {
+
+int32_t prefill_entry(void* out, int64_t out_tok_stride, int64_t out_head_stride, const void* q,
+                      int64_t q_tok_stride, int64_t q_head_stride, const void* k,
+                      int64_t k_tok_stride, int64_t k_head_stride, const void* v,
+                      int64_t v_tok_stride, int64_t v_head_stride, const int32_t* q_start,
+                      const int32_t* q_len, const int32_t* k_start, const int32_t* k_len,
+                      int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                      int32_t num_kv_heads, int32_t head_dim, float scale, int32_t causal,
+                      int32_t dtype, const float* mask, int64_t mask_seq_stride,
+                      int64_t mask_head_stride, int64_t mask_q_stride, void* stream) {
   if (num_seqs < 0 || max_q_len < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       num_heads % num_kv_heads != 0)
     return NIA_ERR_INVALID_ARGUMENT;
@@ -960,6 +1009,11 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
   if (!out || !q || !k || !v || !q_start || !q_len || !k_start || !k_len)
     return NIA_ERR_INVALID_ARGUMENT;
   if (!supported_head_dim(head_dim)) return NIA_ERR_UNSUPPORTED;
+  // the mask is read four keys (16 bytes) at a time
+  if (mask && ((uintptr_t)mask % 16 || mask_seq_stride % 4 || mask_head_stride % 4 ||
+               mask_q_stride % 4 || mask_seq_stride < 0 || mask_head_stride < 0 ||
+               mask_q_stride < 0))
+    return NIA_ERR_MISALIGNED;
   if (dtype == NIA_DTYPE_F32) {
     if (!vec_ok_f32(q, q_tok_stride, q_head_stride) || !vec_ok_f32(k, k_tok_stride, k_head_stride) ||
         !vec_ok_f32(v, v_tok_stride, v_head_stride) ||
@@ -987,6 +1041,10 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
     f.group = num_heads / num_kv_heads;
     f.causal = causal;
     f.scale_log2 = (double)scale * 1.4426950408889634;
+    f.bias = mask;
+    f.bias_seq = mask_seq_stride;
+    f.bias_head = mask_head_stride;
+    f.bias_q = mask_q_stride;
     return launch_prefill_f32(f, false, head_dim, num_seqs, max_q_len, (hipStream_t)stream);
   }
   if (dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
@@ -1021,6 +1079,14 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
   // Every workgroup of a sequence does about the same work unless the mask is the
   // top-left causal triangle: those grids go out longest sequence first.
   p.order_by_len = causal != NIA_CAUSAL_TOP_LEFT && num_seqs <= kOrderMaxSeqs;
+  if (mask) {
+    p.bias = mask;
+    p.bias_seq = mask_seq_stride;
+    p.bias_head = mask_head_stride;
+    p.bias_q = mask_q_stride;
+    p.scale = scale;
+    return launch_prefill<false, true>(p, head_dim, num_seqs, (hipStream_t)stream);
+  }
   // Short unmasked sequences with one query head per KV head (the vision windows):
   // two heads per workgroup, 64 rows each (see prefill_dma_kernel's PAIR mode).
   if (causal == NIA_CAUSAL_NONE && num_heads == num_kv_heads && num_kv_heads % 2 == 0 &&
@@ -1049,6 +1115,42 @@ extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_he
     return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
   }
   return launch_prefill<false>(p, head_dim, num_seqs, (hipStream_t)stream);
+}
+
+}  // namespace
+
+extern "C" int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                               const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                               const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                               const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                               const int32_t* q_start, const int32_t* q_len,
+                               const int32_t* k_start, const int32_t* k_len, int32_t num_seqs,
+                               int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, float scale, int32_t causal, int32_t dtype,
+                               void* stream) {
+  return prefill_entry(out, out_tok_stride, out_head_stride, q, q_tok_stride, q_head_stride, k,
+                       k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, q_start,
+                       q_len, k_start, k_len, num_seqs, max_q_len, num_heads, num_kv_heads,
+                       head_dim, scale, causal, dtype, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" int32_t nia_prefill_masked(void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                      const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                      const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                      const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                      const int32_t* q_start, const int32_t* q_len,
+                                      const int32_t* k_start, const int32_t* k_len,
+                                      int32_t num_seqs, int32_t max_q_len, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, float scale,
+                                      int32_t causal, int32_t dtype, const float* mask,
+                                      int64_t mask_seq_stride, int64_t mask_head_stride,
+                                      int64_t mask_q_stride, void* stream) {
+  if (!mask) return NIA_ERR_INVALID_ARGUMENT;
+  return prefill_entry(out, out_tok_stride, out_head_stride, q, q_tok_stride, q_head_stride, k,
+                       k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, q_start,
+                       q_len, k_start, k_len, num_seqs, max_q_len, num_heads, num_kv_heads,
+                       head_dim, scale, causal, dtype, mask, mask_seq_stride, mask_head_stride,
+                       mask_q_stride, stream);
 }
 
 extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,

@@ -30,6 +30,10 @@ struct PrefillF32Params {
   int32_t causal;
   int32_t decode;  // one query row per sequence: row s of q / o (q_start, q_len unused)
   double scale_log2;
+  // additive mask (contiguous mode, optional): bias[s * bias_seq + h * bias_head +
+  // i * bias_q + j] joins the scaled score of query row i and key j
+  const float* bias;
+  int64_t bias_seq, bias_head, bias_q;
 };
 
 // Grid (m-blocks of 64 rows, heads, sequences); returns an NIA_* status.

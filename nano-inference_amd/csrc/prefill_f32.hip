@@ -103,6 +103,9 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
   float l_run = 0.f;         // this lane's share of the query's sum
 
   const int32_t* bt = PAGED ? p.block_tables + (int64_t)seq * p.bt_stride : nullptr;
+  const float* bias_row = p.bias ? p.bias + (int64_t)seq * p.bias_seq + (int64_t)h * p.bias_head +
+                                       (int64_t)(row_ok ? r : 0) * p.bias_q
+                                 : nullptr;
   for (int n0 = 0; n0 < n_end; n0 += kF32BlockN) {
     __syncthreads();  // the previous tile is consumed
     // ---- stage keys n0 .. n0 + 31 (zeros past the context and in invalid blocks) ----------
@@ -162,6 +165,8 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
         const int key = 16 * kt + 4 * i + slot;
         const bool vis = n0 + key < kb && sok[key];
         x[kt][i] = vis ? s[kt][i] * p.scale_log2 : -INFINITY;
+        if (!PAGED && p.bias && vis)
+          x[kt][i] += (double)bias_row[n0 + key] * 1.4426950408889634;
         mx = fmax(mx, x[kt][i]);
       }
     mx = fmax(mx, __shfl_xor(mx, 16, kWave));

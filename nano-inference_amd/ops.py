@@ -486,13 +486,16 @@ def prefill(
     causal: int = CAUSAL_TOP_LEFT,
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    mask: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Varlen attention over contiguous K/V rows (nia_prefill), bf16 or fp32.
 
     q/out: (Tq, H, D); k/v: (Tk, H_kv, D), each with a contiguous last dim.
     Sequence s owns query rows q_start[s] .. + q_len[s] and key rows
     k_start[s] .. + k_len[s].  ``causal`` is CAUSAL_NONE / CAUSAL_TOP_LEFT /
-    CAUSAL_BOTTOM_RIGHT (see include/nia_attn.h).
+    CAUSAL_BOTTOM_RIGHT (see include/nia_attn.h).  ``mask`` (optional, nia_prefill_masked):
+    an additive float mask indexed [sequence, head, query row, key] (size-1 dimensions
+    broadcast), added to the scaled scores; -inf masks a key.
     """
     dev = _require_gpu(q, k, v, q_start, q_len, k_start, k_len)
     if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape:
@@ -517,6 +520,19 @@ def prefill(
     elif out.shape != q.shape or out.dtype != q.dtype:
         raise ValueError("out must match q's shape and dtype")
     _last_contig("out", out)
+    if mask is not None:
+        m4, strides = _mask_operand(mask, n, h, dev)
+        st = _lib.load().nia_prefill_masked(
+            out.data_ptr(), out.stride(0), out.stride(1),
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), k.stride(0), k.stride(1),
+            v.data_ptr(), v.stride(0), v.stride(1),
+            qs.data_ptr(), ql.data_ptr(), ks.data_ptr(), kl.data_ptr(),
+            n, int(max_q_len), h, hkv, d, _default_scale(d, scale), int(causal), dt,
+            m4.data_ptr(), *strides, _stream(dev),
+        )
+        _lib.check("nia_prefill_masked", st)
+        return out
     lib = _lib.calls()
     st = lib.nia_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
@@ -528,6 +544,31 @@ def prefill(
     )
     _lib.check("nia_prefill", st)
     return out
+
+
+def _mask_operand(mask: torch.Tensor, num_seqs: int, num_heads: int, device):
+    """A 4-D additive mask [S or 1, H or 1, rows, keys] as the fp32 operand of
+    nia_prefill_masked: 16-byte aligned, last dimension contiguous and every stride a
+    multiple of four elements (a copy with the key dimension padded to a multiple of four
+    when the given tensor is not); returns it and its (sequence, head, row) strides, 0
+    for broadcast dimensions."""
+    if mask.dim() != 4:
+        raise ValueError(f"mask must be 4-D [sequences, heads, rows, keys], got {tuple(mask.shape)}")
+    if mask.shape[0] not in (1, num_seqs) or mask.shape[1] not in (1, num_heads):
+        raise ValueError(f"mask of shape {tuple(mask.shape)} for {num_seqs} sequences and "
+                         f"{num_heads} heads")
+    m = mask.to(device=device, dtype=torch.float32)
+    st = m.stride()
+    ok = (m.stride(3) == 1 or m.shape[3] == 1) and m.data_ptr() % 16 == 0 and all(
+        (st[i] % 4 == 0 or m.shape[i] == 1) for i in range(3))
+    if not ok:
+        keys = m.shape[3]
+        padded = torch.zeros(*m.shape[:3], -(-keys // 4) * 4, dtype=torch.float32,
+                             device=device)
+        padded[..., :keys] = m
+        m = padded
+    strides = tuple(0 if m.shape[i] == 1 else m.stride(i) for i in range(3))
+    return m, strides
 
 
 def varlen_attention(

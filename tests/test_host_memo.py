@@ -1,5 +1,6 @@
 """Host-side memo of results that read a tensor back (ops.TensorMemo), as used for the
-prefix-mask check of the layers and the max chunk length of varlen attention: one
+prefix-mask check of the layers (and the general additive path other masks take) and the
+max chunk length of varlen attention: one
 device read per tensor, recomputed when the tensor is modified in place, never reused
 for another tensor.  Runs on the CPU (the memo and the mask check are device-agnostic).
 """
@@ -40,14 +41,39 @@ def test_prefix_lengths_checked_once_per_mask():
     assert A._prefix_lengths(mask, 2, 4, cpu).tolist() == [3, 3]
 
 
-def test_non_prefix_masks_still_raise_every_time():
+def test_non_prefix_masks_go_to_the_general_path():
+    """A mask that is not a prefix gives no key lengths (None, memoised too), and the
+    additive form the reference adds to the scores (attention.py:40-47) is built for it:
+    a 2-D bool mask as 0 / -inf, a float mask cast to the scores' dtype, broadcastable."""
     cpu = torch.device("cpu")
     bad = torch.tensor([[1, 0, 1, 0]], dtype=torch.bool)
     for _ in range(2):
-        with pytest.raises(NotImplementedError, match="prefix"):
-            A._prefix_lengths(bad, 1, 4, cpu)
-    with pytest.raises(NotImplementedError, match="shape"):
-        A._prefix_lengths(torch.ones(1, 2, 1, 4), 1, 4, cpu)
+        assert A._prefix_lengths(bad, 1, 4, cpu) is None
+    assert A._prefix_lengths(torch.ones(1, 2, 1, 4), 1, 4, cpu) is None
+    soft = torch.zeros(1, 1, 1, 4)
+    soft[0, 0, 0, 1] = -2.5  # finite, non-zero: an additive bias, not a visibility mask
+    assert A._prefix_lengths(soft, 1, 4, cpu) is None
+    add = A._additive_mask(bad, 1, 3, 2, 4, torch.bfloat16)
+    assert add.shape == (1, 1, 1, 4) and add.dtype == torch.bfloat16
+    assert add[0, 0, 0].tolist() == [0.0, float("-inf"), 0.0, float("-inf")]
+    wide = torch.randn(2, 3, 5, 7)
+    got = A._additive_mask(wide, 2, 3, 5, 6, torch.float32)  # sliced to S_k = 6
+    assert torch.equal(got, wide[..., :6])
+    with pytest.raises(ValueError, match="broadcast"):
+        A._additive_mask(torch.zeros(2, 4, 5, 6), 2, 3, 5, 6, torch.float32)
+
+
+def test_mask_operand_alignment_and_broadcast_strides():
+    """ops._mask_operand: fp32, rows whose strides are multiples of four elements (a copy
+    with keys padded to four when needed), and stride 0 for broadcast dimensions."""
+    m = torch.randn(1, 3, 1, 6)  # 6 keys: rows of 6 floats are not 16-byte multiples
+    op, st = ops._mask_operand(m, 2, 3, torch.device("cpu"))
+    assert op.dtype == torch.float32 and op.shape[-1] == 8 and st[0] == 0 and st[2] == 0
+    assert st[1] % 4 == 0 and torch.equal(op[..., :6], m)
+    op2, st2 = ops._mask_operand(torch.zeros(2, 1, 4, 8), 2, 5, torch.device("cpu"))
+    assert st2 == (32, 0, 8) and op2.shape == (2, 1, 4, 8)
+    with pytest.raises(ValueError):
+        ops._mask_operand(torch.zeros(3, 1, 4, 8), 2, 5, torch.device("cpu"))
 
 
 def test_varlen_max_seqlen_memo():
