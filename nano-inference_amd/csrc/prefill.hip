@@ -580,7 +580,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   const int wave_kend = r0 < qlen ? (causal ? min(klen, q_pos0 + min(r0 + 32, qlen)) : klen) : 0;
 
   uint4 qreg[DK];
-  {
+  if constexpr (PAIR) {
     const bf16_t* qp = p.q + (qstart + (row_ok ? qrow : 0)) * p.q_tok + (int64_t)h * p.q_head;
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk)
@@ -898,9 +898,36 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   } else if (n_end > 0) {
   // ---- main loop: tile n0 in one stage while tile n0 + 64 streams into the other ---------
   // Unrolled by two so that each stage's LDS offsets are compile-time constants.
+    // This wave's 32 query rows stream into stage 1 (free until tile 1 streams in) by DMA,
+    // whole rows per instruction, through the K tiles' swizzle; they are then read in the
+    // B-operand layout exactly as the K operand is.  Rows past the sequence repeat its last
+    // row (finite data, their outputs are never stored).
+    uint8_t* qbuf = (wave < 2 ? lds_k1 : lds_v1) + (wave & 1) * (32 * kTileRowBytes);
+    if (r0 < qlen) {
+#pragma unroll
+      for (int grp = 0; grp < 2; ++grp) {
+        const int g0 = r0 + 16 * grp;
+        const int gk = min(g0, qlen - 1);
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(p.q + (qstart + gk) * p.q_tok + (int64_t)h * p.q_head), 0,
+            (int)((15 * p.q_tok + D) * 2), kBufferWord3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * i + ld_sub;
+          const int dr = min(g0 + r, qlen - 1) - gk;
+          if (kChunks == 16 || chunk_ok[i])
+            lds_dma16(rq, (uint32_t)(dr * p.q_tok + 8 * (ld_pc ^ tile_swz(r))) * 2u,
+                      qbuf + grp * 16 * kTileRowBytes + i * 1024);
+        }
+      }
+    }
     int blk_nxt = block_of(0);
     issue_tile(0, 0, blk_nxt);
     if (kBlockN < n_end) blk_nxt = block_of(kBlockN);
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk)
+      qreg[kk] = row_ok ? *reinterpret_cast<const uint4*>(qbuf + k_off[kk]) : make_uint4(0, 0, 0, 0);
     auto step = [&](int n0, auto stage_c) __attribute__((always_inline)) {
       constexpr int kStage = decltype(stage_c)::value;
       __builtin_amdgcn_s_waitcnt(0);
@@ -949,9 +976,10 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
   const dim3 grid((unsigned)nwg);
   // The DMA kernel needs 16-row groups inside one KV block and 32-bit lane offsets;
   // the register-staged kernel serves the rest.
-  const bool dma_ok = PAGED ? p.bs_log2 >= 4
-                            : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
-                               p.v_tok < kMaxRowStride);
+  const bool dma_ok = p.q_tok >= 0 && p.q_tok < kMaxRowStride &&
+                      (PAGED ? p.bs_log2 >= 4
+                             : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
+                                p.v_tok < kMaxRowStride));
   if (BIAS && !dma_ok) return NIA_ERR_UNSUPPORTED;
   switch (head_dim) {
 #define NIA_PREFILL_CASE(DD)                                                                 \
