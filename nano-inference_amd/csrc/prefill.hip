@@ -503,11 +503,16 @@ constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
 // workgroups, none of them with idle waves.
 // BIAS (contiguous K/V, no pairing): an additive fp32 mask joins the scaled scores, which
 // are then carried in nats (exponent scale log2 e instead of scale * log2 e).
-template <int D, bool PAGED, bool PAIR = false, bool BIAS = false>
-__global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(PrefillParams p) {
+// COMPACT (paired heads, D < 128): K/V rows keep their own D * 2 bytes in LDS (no swizzle)
+// instead of 256, so three workgroups fit a CU instead of two: the short windows are bound
+// by the latency of their loads, which more resident workgroups hide.
+template <int D, bool PAGED, bool PAIR = false, bool BIAS = false, bool COMPACT = false>
+__global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_kernel(
+    PrefillParams p) {
   static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
   static_assert(!(PAIR && PAGED), "paired heads read contiguous K/V");
   static_assert(!(BIAS && (PAIR || PAGED)), "masks apply to contiguous, unpaired calls");
+  static_assert(!COMPACT || (PAIR && D < 128), "compact rows serve paired heads, D < 128");
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
@@ -515,14 +520,20 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   // sums instead of the vector unit.  Those V columns are never written by the DMA; they
   // hold 1.0 at dim D and zeros, so O^T row D accumulates sum_k P[k] with O's own
   // rescales, and the lazy check tests the largest exponent instead of a lane sum.
-  constexpr bool kSumRow = D % 32 == 16;
+  constexpr bool kSumRow = D % 32 == 16 && !COMPACT;
+  // bytes per K/V row in LDS, and the chunk swizzle (none for compact rows; the last P.V
+  // tile's padded dims then read the next row's data, finite, and are never stored, and
+  // 64 bytes past each tile keep the last row's overreach inside the array)
+  constexpr int kPitch = COMPACT ? 2 * D : kTileRowBytes;
+  constexpr int kTileSz = COMPACT ? kBlockN * kPitch + 64 : kTileBytes;
+  auto swz = [](int r) __attribute__((always_inline)) { return COMPACT ? 0 : tile_swz(r); };
   // One array per stage and operand: the compiler then sees that the DMA into one stage
   // cannot alias the LDS reads of the other and issues no vmcnt wait before those reads
   // (with one [stage][K, V] array it waited for the next tile's DMA inside every tile).
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_k0[kTileSz];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v0[kTileSz];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_k1[kTileSz];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_v1[kTileSz];
   auto tile_k = [&](int stage) __attribute__((always_inline)) { return stage ? lds_k1 : lds_k0; };
   auto tile_v = [&](int stage) __attribute__((always_inline)) { return stage ? lds_v1 : lds_v0; };
 
@@ -670,6 +681,24 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
       }
     }
   };
+  // COMPACT: this wave's 32 rows of tile n0 (rows 32 wrow ..), row after row at D * 2 bytes
+  // each, a DMA instruction covering 1 KB of them; rows past the context repeat the last key.
+  auto issue_compact = [&](const bf16_t* base, int64_t tok, int64_t head, uint8_t* tile,
+                           int n0) __attribute__((always_inline)) {
+    const int g0 = n0 + 32 * wrow;
+    const int gk = min(g0, klen - 1);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(base + (kstart + gk) * tok + (int64_t)hk * head), 0, (int)((31 * tok + D) * 2),
+        kBufferWord3);
+#pragma unroll
+    for (int t = 0; t < kChunks / 2; ++t) {  // 32 rows x kChunks chunks / 64 lanes
+      const int u = 64 * t + lane;
+      const int r = u / kChunks;
+      const int ch = u - r * kChunks;
+      const int dr = min(g0 + r, klen - 1) - gk;
+      lds_dma16(rsrc, (uint32_t)(dr * tok + 8 * ch) * 2u, tile + 32 * wrow * kPitch + 1024 * t);
+    }
+  };
   auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
     issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, tile_k(stage), n0, blk, wave);
     issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, tile_v(stage), n0, blk, wave);
@@ -680,7 +709,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   int k_off[DK];
 #pragma unroll
   for (int kk = 0; kk < DK; ++kk)
-    k_off[kk] = col * kTileRowBytes + 16 * ((2 * kk + half) ^ tile_swz(col));
+    k_off[kk] = col * kPitch + 16 * ((2 * kk + half) ^ swz(col));
   // V^T operand via transposed reads: 16-lane group g reads rows
   // 16 kc + 4 (g / 2) + i / 4 (+ 8 for the second read), dims
   // 32 dt + 16 (g % 2) + 4 (i % 4) .. + 3, i = lane % 16.
@@ -692,9 +721,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
   int v_off[DT], v_off2[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
-    v_off[dt] = vr15 * kTileRowBytes + 16 * ((4 * dt + vcd) ^ tile_swz(vr15)) + 8 * (i16 & 1);
+    v_off[dt] = vr15 * kPitch + 16 * ((4 * dt + vcd) ^ swz(vr15)) + 8 * (i16 & 1);
     v_off2[dt] =
-        (vr15 + 8) * kTileRowBytes + 16 * ((4 * dt + vcd) ^ tile_swz(vr15 + 8)) + 8 * (i16 & 1);
+        (vr15 + 8) * kPitch + 16 * ((4 * dt + vcd) ^ swz(vr15 + 8)) + 8 * (i16 & 1);
   }
 
   // the exponent scale of the scores as the tile carries them
@@ -711,7 +740,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     for (int kk = 0; kk < DK; ++kk) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kTileRowBytes + k_off[kk]);
+        const uint4 a = *reinterpret_cast<const uint4*>(kt + c * 32 * kPitch + k_off[kk]);
         // raw scores q . k in fp32 (the bf16 products are exact)
         sacc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, qreg[kk]),
@@ -799,8 +828,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
         const uint4 pbk = make_uint4(w[0], w[1], w[2], w[3]);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const s16x4_t lo = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off[dt]);
-          const s16x4_t hi = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off2[dt]);
+          const s16x4_t lo = lds_read_tr16(vt + kc * 16 * kPitch + v_off[dt]);
+          const s16x4_t hi = lds_read_tr16(vt + kc * 16 * kPitch + v_off2[dt]);
           const s16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, pbk), oacc[dt], 0,
@@ -862,8 +891,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const s16x4_t lo = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off[dt]);
-        const s16x4_t hi = lds_read_tr16(vt + kc * 16 * kTileRowBytes + v_off2[dt]);
+        const s16x4_t lo = lds_read_tr16(vt + kc * 16 * kPitch + v_off[dt]);
+        const s16x4_t hi = lds_read_tr16(vt + kc * 16 * kPitch + v_off2[dt]);
         const s16x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, pb[kc]), oacc[dt], 0,
@@ -886,10 +915,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_dma_kernel(Prefill
     const int hsel = wave >> 1;
     for (int n0 = 0; n0 < n_end; n0 += kBlockN) {
       if (n0 > 0) __syncthreads();  // every wave is done with the previous tile
+      if constexpr (COMPACT) {
+        issue_compact(p.k, p.k_tok, p.k_head, tile_k(hsel), n0);
+        issue_compact(p.v, p.v_tok, p.v_head, tile_v(hsel), n0);
+      } else {
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, tile_k(hsel), n0, 0, 2 * wrow + g);
-        issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, tile_v(hsel), n0, 0, 2 * wrow + g);
+        for (int g = 0; g < 2; ++g) {
+          issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, tile_k(hsel), n0, 0, 2 * wrow + g);
+          issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, tile_v(hsel), n0, 0, 2 * wrow + g);
+        }
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
@@ -1129,7 +1163,7 @@ int32_t prefill_entry(void* out, int64_t out_tok_stride, int64_t out_head_stride
     switch (head_dim) {
 #define NIA_PAIR_CASE(DD)                                                                       \
   case DD:                                                                                      \
-    nia_launch((prefill_dma_kernel<DD, false, true>), dim3((unsigned)nwg),                      \
+    nia_launch((prefill_dma_kernel<DD, false, true, false, (DD < 128)>), dim3((unsigned)nwg),   \
                dim3(kPrefillThreads), st, p);                                                   \
     break;
       NIA_PAIR_CASE(64)
