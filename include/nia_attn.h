@@ -180,7 +180,8 @@ int32_t nia_prefill(void* out, int64_t out_tok_stride, int64_t out_head_stride,
  * key j of sequence s and query head h is
  *     mask[s * mask_seq_stride + h * mask_head_stride + i * mask_q_stride + j]
  * (element strides, multiples of 4 and >= 0; 0 broadcasts), read for keys j < k_len[s]
- * and rows i < q_len[s] only.  -inf masks a key; the causal mode still applies.  A row
+ * and rows i < q_len[s] only; the library cannot see the mask's extent, so every such
+ * element must lie inside it (the Python op checks the shape first).  -inf masks a key; the causal mode still applies.  A row
  * whose every key is masked produces zeros (the reference's softmax gives NaN there).
  * Same support as nia_prefill, except that bf16 K/V token strides must stay below 2^26
  * elements (else NIA_ERR_UNSUPPORTED); mask == NULL returns NIA_ERR_INVALID_ARGUMENT.

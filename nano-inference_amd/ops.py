@@ -521,7 +521,10 @@ def prefill(
         raise ValueError("out must match q's shape and dtype")
     _last_contig("out", out)
     if mask is not None:
-        m4, strides = _mask_operand(mask, n, h, dev)
+        # the mask must cover every key the kernels read: one read of the key lengths (general
+        # masks are rare; prefix masks take the key-length path and never come here)
+        max_keys = int(kl.max()) if n > 0 else 0
+        m4, strides = _mask_operand(mask, n, h, int(max_q_len), max_keys, dev)
         st = _lib.load().nia_prefill_masked(
             out.data_ptr(), out.stride(0), out.stride(1),
             q.data_ptr(), q.stride(0), q.stride(1),
@@ -546,17 +549,29 @@ def prefill(
     return out
 
 
-def _mask_operand(mask: torch.Tensor, num_seqs: int, num_heads: int, device):
+def _mask_operand(mask: torch.Tensor, num_seqs: int, num_heads: int, max_rows: int,
+                  max_keys: int, device):
     """A 4-D additive mask [S or 1, H or 1, rows, keys] as the fp32 operand of
     nia_prefill_masked: 16-byte aligned, last dimension contiguous and every stride a
     multiple of four elements (a copy with the key dimension padded to a multiple of four
     when the given tensor is not); returns it and its (sequence, head, row) strides, 0
-    for broadcast dimensions."""
+    for broadcast dimensions.  The kernels read rows below ``max_rows`` (the launch's
+    longest query run) and keys below each sequence's key length (at most ``max_keys``),
+    so a mask must cover them: a row or key dimension of size 1 broadcasts, and one that
+    is shorter raises ValueError here instead of reading past the tensor."""
     if mask.dim() != 4:
         raise ValueError(f"mask must be 4-D [sequences, heads, rows, keys], got {tuple(mask.shape)}")
     if mask.shape[0] not in (1, num_seqs) or mask.shape[1] not in (1, num_heads):
         raise ValueError(f"mask of shape {tuple(mask.shape)} for {num_seqs} sequences and "
                          f"{num_heads} heads")
+    if mask.shape[2] != 1 and mask.shape[2] < max_rows:
+        raise ValueError(f"mask of shape {tuple(mask.shape)} has fewer rows than the "
+                         f"{max_rows} queries of the longest sequence")
+    if mask.shape[3] != 1 and mask.shape[3] < max_keys:
+        raise ValueError(f"mask of shape {tuple(mask.shape)} has fewer keys than the "
+                         f"{max_keys} of the longest sequence")
+    if mask.shape[3] == 1 and max_keys > 1:
+        mask = mask.expand(*mask.shape[:3], max_keys)  # the kernels read keys as a row
     m = mask.to(device=device, dtype=torch.float32)
     st = m.stride()
     ok = (m.stride(3) == 1 or m.shape[3] == 1) and m.data_ptr() % 16 == 0 and all(

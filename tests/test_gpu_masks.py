@@ -139,3 +139,28 @@ def test_prefix_masks_still_take_the_key_length_path():
     assert_attn_close(out_prefix, oracle(q, k, v, add.double(), True), torch.bfloat16, "prefix")
     assert_attn_close(out_mask.view(b, s, h, d).transpose(1, 2),
                       oracle(q, k, v, add.double(), True), torch.bfloat16, "as a mask")
+
+
+def test_varlen_masks_cover_rows_and_keys_or_raise():
+    """ops.prefill with a mask over ragged sequences: a mask with fewer keys than the longest
+    sequence's, or fewer rows than the longest query run, raises ValueError before any launch
+    (the kernels would read past it); a key-broadcast mask ([S, 1, rows, 1], one bias per
+    query row) gives the unmasked attention, since softmax ignores a per-row constant."""
+    lens = [5, 9]
+    t = sum(lens)
+    g = torch.Generator(device="cuda").manual_seed(77)
+    q = torch.randn((t, 2, 64), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((t, 2, 64), generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn((t, 2, 64), generator=g, device="cuda").to(torch.bfloat16)
+    st = torch.tensor([0, 5], dtype=torch.int32, device="cuda")
+    ln = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    args = (q, k, v, st, ln, st, ln, 9, ops.CAUSAL_NONE)
+    with pytest.raises(ValueError, match="keys"):
+        ops.prefill(*args, mask=torch.zeros(2, 1, 9, 8, device="cuda"))
+    with pytest.raises(ValueError, match="rows"):
+        ops.prefill(*args, mask=torch.zeros(2, 1, 8, 9, device="cuda"))
+    plain = ops.prefill(*args)
+    per_row = torch.randn(2, 1, 9, 1, generator=g, device="cuda")
+    got = ops.prefill(*args, mask=per_row)
+    torch.cuda.synchronize()
+    assert (got.float() - plain.float()).abs().max().item() < 2e-2

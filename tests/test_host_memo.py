@@ -67,13 +67,31 @@ def test_mask_operand_alignment_and_broadcast_strides():
     """ops._mask_operand: fp32, rows whose strides are multiples of four elements (a copy
     with keys padded to four when needed), and stride 0 for broadcast dimensions."""
     m = torch.randn(1, 3, 1, 6)  # 6 keys: rows of 6 floats are not 16-byte multiples
-    op, st = ops._mask_operand(m, 2, 3, torch.device("cpu"))
+    op, st = ops._mask_operand(m, 2, 3, 5, 6, torch.device("cpu"))
     assert op.dtype == torch.float32 and op.shape[-1] == 8 and st[0] == 0 and st[2] == 0
     assert st[1] % 4 == 0 and torch.equal(op[..., :6], m)
-    op2, st2 = ops._mask_operand(torch.zeros(2, 1, 4, 8), 2, 5, torch.device("cpu"))
+    op2, st2 = ops._mask_operand(torch.zeros(2, 1, 4, 8), 2, 5, 4, 8, torch.device("cpu"))
     assert st2 == (32, 0, 8) and op2.shape == (2, 1, 4, 8)
     with pytest.raises(ValueError):
-        ops._mask_operand(torch.zeros(3, 1, 4, 8), 2, 5, torch.device("cpu"))
+        ops._mask_operand(torch.zeros(3, 1, 4, 8), 2, 5, 4, 8, torch.device("cpu"))
+
+
+def test_mask_operand_covers_the_rows_and_keys_the_kernels_read():
+    """A mask with fewer rows than the longest query run or fewer keys than the longest key
+    run raises (the kernels would read past it); size-1 row and key dimensions broadcast,
+    the key dimension materialised (the kernels read a mask row's keys as a row)."""
+    cpu = torch.device("cpu")
+    with pytest.raises(ValueError, match="rows"):
+        ops._mask_operand(torch.zeros(1, 1, 4, 8), 1, 2, 5, 8, cpu)
+    with pytest.raises(ValueError, match="keys"):
+        ops._mask_operand(torch.zeros(1, 1, 5, 8), 1, 2, 5, 9, cpu)
+    m = torch.randn(2, 1, 1, 1)
+    op, st = ops._mask_operand(m, 2, 3, 5, 7, cpu)
+    assert op.shape == (2, 1, 1, 8) and st[1] == 0 and st[2] == 0 and st[0] % 4 == 0
+    assert torch.equal(op[..., :7], m.expand(2, 1, 1, 7))
+    # longer masks are fine (the kernels read a prefix of every row)
+    op3, _ = ops._mask_operand(torch.zeros(1, 2, 9, 12), 1, 2, 5, 8, cpu)
+    assert op3.shape == (1, 2, 9, 12)
 
 
 def test_varlen_max_seqlen_memo():
