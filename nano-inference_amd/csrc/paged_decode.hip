@@ -640,6 +640,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   __shared__ int s_pfx[kSplitLdsBatch + 1];
   __shared__ int s_ctx[kSplitLdsBatch];
   __shared__ int s_wave[kDecodeWaves];
+  // The parameters of the prologue and the first unit in one round of scalar loads (left to
+  // itself the compiler loads each on first use, a round trip each before the first DMA).
+  asm volatile("" ::"s"(p.context_lens), "s"(p.max_blocks), "s"(p.bs_log2), "s"(p.ws_pfx),
+               "s"(p.grid), "s"(p.first_wgs), "s"(p.wph), "s"(p.hg), "s"(p.nhg),
+               "s"(p.block_tables), "s"(p.bt_stride), "s"(p.group));
+  asm volatile("" ::"s"(p.k_cache), "s"(p.v_cache), "s"(p.num_kv_heads), "s"(p.num_blocks),
+               "s"(p.q), "s"(p.q_b), "s"(p.q_h), "s"(p.q_group));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   // wave-uniform, and said so: everything derived from it (the unit walk, block ids, buffer
@@ -1101,17 +1108,26 @@ template <int D, bool FP8>
 __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(DecodeParams p,
                                                                                int batch) {
   static_assert(D <= 2 * kWave, "two output dims per lane");
+  // Every parameter, and then the pair's three prefix entries, in one round of loads each:
+  // left to itself the compiler loads each parameter on first use, behind the branches, and
+  // the short kernel is a chain of such round trips.
+  asm volatile("" ::"s"(p.num_heads), "s"(p.group), "s"(p.hg), "s"(p.ws_pfx), "s"(p.out),
+               "s"(p.out_b), "s"(p.out_h), "s"(p.q_group), "s"(p.nhg), "s"(p.first_wgs),
+               "s"(p.wph), "s"(p.grid), "s"(p.sp_ml), "s"(p.sp_o));
   const int lane = threadIdx.x & (kWave - 1);
   const int pair = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6);
-  if (pair >= batch * p.num_heads) return;
   const int b = pair / p.num_heads;
+  const int bl = b < batch ? b : batch - 1;  // the loads stay inside the prefix
+  const int T = p.ws_pfx[batch];
+  const int pb = p.ws_pfx[bl];
+  const int pb1 = p.ws_pfx[bl + 1];
+  asm volatile("" ::"v"(pb), "v"(pb1), "s"(T));
+  if (pair >= batch * p.num_heads) return;
   const int h = pair - b * p.num_heads;
   const int G = p.group;
   const int hk = h / G, gq = h - hk * G;
   const int g = hk / p.hg, hig = hk - g * p.hg;
-  const int T = p.ws_pfx[batch];
-  const int pb = p.ws_pfx[b];
-  const int n_units = p.ws_pfx[b + 1] - pb;
+  const int n_units = pb1 - pb;
   const int d0 = 2 * lane;
   const bool has_dims = d0 < D;
   bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)b * p.out_b +
