@@ -489,13 +489,17 @@ __global__ __launch_bounds__(kCombineThreads) void paged_decode_combine_kernel(D
   out[1] = E::from_f32(acc.y * inv);
 }
 
-// Inclusive prefix sum over the lanes of a wave.
-NIA_DEVICE int wave_inclusive_scan(int x, int lane) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(x, off, kWave);
-    if (lane >= off) x += y;
-  }
+// Inclusive prefix sum over the lanes of a wave, by DPP moves (no LDS round trips): shifts
+// of 1, 2, 4 and 8 lanes inside each row of 16, then row 0's total added to row 1 and row
+// 2's to row 3 (row_bcast:15), then rows 0-1's total to rows 2 and 3 (row_bcast:31).  Lanes
+// whose source lies outside the row, and rows outside the row mask, add 0.
+NIA_DEVICE int wave_inclusive_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2, 3
   return x;
 }
 
@@ -504,7 +508,7 @@ NIA_DEVICE int wave_inclusive_scan(int x, int lane) {
 NIA_DEVICE int block_exclusive_scan(int v, int* s_wave, int& total) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int inc = wave_inclusive_scan(v, lane);
+  const int inc = wave_inclusive_scan(v);
   if (lane == kWave - 1) s_wave[wave] = inc;
   __syncthreads();
   int base = 0, tot = 0;
