@@ -126,8 +126,9 @@ int32_t nia_paged_decode(void* out, int64_t out_batch_stride, int64_t out_head_s
  * memory (one per GPU, held until the process ends).  A call whose
  * nia_paged_decode_workspace_size(...) exceeds it returns NIA_ERR_SCRATCH_LIMIT before
  * anything is launched.  40 MiB holds every bf16 layout the split kernel takes (up to
- * 16 query heads per KV head at head_dim 128: 34.1 MB of partials) for batches up to
- * 1.9 million sequences; fp32 calls need batch x num_heads x ceil(max_blocks / 32) x
+ * 16 query heads per KV head at head_dim 128: 34.1 MB of partials) with 4 + 8 x
+ * num_kv_heads bytes per sequence beside them, i.e. batches up to 115,000 sequences at 8
+ * KV heads; fp32 calls need batch x num_heads x ceil(max_blocks / 32) x
  * (head_dim + 2) x 4 bytes (plus 256), so long fp32 batches can exceed it.  All calls
  * on one GPU share the array: calls that overlap in time on one GPU (other streams,
  * other threads) race.

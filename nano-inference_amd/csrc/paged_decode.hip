@@ -15,15 +15,17 @@
 //   prefix sum over sequences of their unit counts and T = pfx[batch], built on the
 //   device from context_lens.  A workgroup is 4 waves = hg KV heads x wph = 4 / hg
 //   slices; "virtual wave" vw = w * wph + slice owns one KV head of the group and the
-//   contiguous unit range [total * vw / V, total * (vw + 1) / V), V = grid * wph, of a
-//   grid of resident workgroups.  Every wave streams its range alone (no work queue, no
-//   barrier, no cross-wave merge): pairs of tiles DMA (buffer loads into LDS) into its
-//   16 KB slot one pair ahead, S^T = K Q^T and O^T += V^T P^T run on 16x16 MFMAs with the
-//   group's G <= 16 query heads as columns, and at the end of every sequence of its range
-//   the wave writes the output (it had the whole sequence) or a partial (m, l, o) that
-//   the combine kernel merges.  The ranges are equal, so no workgroup waits on a long
-//   last item, and with hg = 4 the 4 waves of a workgroup read the 4 adjacent KV heads
-//   of the same blocks (16 KB contiguous per block for K and for V).
+//   contiguous unit range [total * W(vw) / W(V), total * W(vw + 1) / W(V)), V = grid *
+//   wph, of a grid of resident workgroups (W sums per-wave weights; RangeWeights).  Every
+//   wave streams its range alone (no work queue, no barrier, no cross-wave merge): pairs
+//   of tiles DMA (buffer loads into LDS) into its 16 KB slot one pair ahead, S^T = K Q^T
+//   and O^T += V^T P^T run on 16x16 MFMAs with the group's G <= 16 query heads as columns,
+//   and at the end of every sequence of its range the wave writes the output (it had the
+//   whole sequence) or a partial (m, l, o), and records which ranges hold the sequence's
+//   first and last unit; the combine kernel merges the partials of those ranges.  The
+//   ranges are weighted so that the waves end together, so no workgroup waits on a long
+//   last item, and with hg = 4 the 4 waves of a workgroup read the 4 adjacent KV heads of
+//   the same blocks (16 KB contiguous per block for K and for V).
 //   Shapes: block size a power of two >= 4 (>= 16 for fp8), head_dim 64 / 80 / 96 / 128
 //   (fp8: 128), any G: groups of more than 16 query heads per KV head run as launches of
 //   at most 16 heads each (the MFMA columns), one after another on the stream.
@@ -84,6 +86,8 @@ struct DecodeParams {
   int32_t grid;   // workgroups
   int32_t first_wgs;  // workgroups dispatched first on their CU
   int32_t* ws_pfx;  // [batch + 1] units before each sequence (one head group)
+  int32_t* ws_rec;  // [nhg][batch][2]: the ranges holding a sequence's first unit (2 v + its
+                    // partial's slot) and its last unit (v), written by the split kernel
   float* sp_ml;     // [grid * wph][2][hg][G] (m, l) of the partial of a range's first / last sequence
   float* sp_o;      // [grid * wph][2][hg][G][D]
 };
@@ -531,50 +535,52 @@ constexpr int kSplitLdsBatch = 1024;   // batches whose unit prefix (and context
                                        // workgroup builds in LDS
 constexpr int kSplitMaxGrid = 512;     // workgroups at most (sizes the partial slots)
 
-// Range weights.  With two workgroups per CU the one dispatched second on its CU (ids
-// grid / 2 and up: the dispatcher fills every CU once before doubling up) streams ~10%
-// slower while both run (measured per workgroup over the Qwen3-8B decode: 0.77 vs 0.85
-// units/us, the same whichever ranges they get), so over bf16 caches the first ones take
-// kRangeFirst / kRangeSecond times as many units and both halves end together (decode
-// kernel 192 -> 187 us).  Over the fp8 format the halves are even (weighting them cost
-// 1.6 us), so its ranges stay equal.  Compile-time constants: read from the parameters,
-// the weights cost the split kernel ~20 scalar-register spills in its loop.
+// Range weights.  Per-wave timelines of the Qwen3-8B decode (time per unit, two boxes) show
+// two kinds of slower waves, whatever ranges they hold: those of the workgroup dispatched
+// second on its CU (ids first_wgs and up: the dispatcher fills every CU once before
+// doubling up) stream ~20% slower than the first one's while both run, and those on the
+// odd-numbered XCDs (workgroup i runs on XCD i % 8) ~8% slower than on the even ones.  Over
+// bf16 caches the four classes (first / second on the CU, even / odd XCD) take units in the
+// ratio 13 : 12 : 11 : 10 (decode kernel and merge 193.2 -> 190.5 us); over the fp8 format
+// the ranges are even (weighting them cost 1.6 us).  Compile-time constants: read from the
+// parameters, the weights cost the split kernel ~20 scalar-register spills in its loop.
 template <bool FP8>
 struct RangeWeights {
-  static constexpr int kFirst = FP8 ? 1 : 6;
-  static constexpr int kSecond = FP8 ? 1 : 5;
+  static constexpr int kFirstEven = FP8 ? 1 : 13, kFirstOdd = FP8 ? 1 : 12;
+  static constexpr int kSecondEven = FP8 ? 1 : 11, kSecondOdd = FP8 ? 1 : 10;
 };
 
-// The ranges: virtual wave v starts at unit floor(total * W(v) / W(V)), where W sums the
-// weights of the virtual waves before v (the first `first` of them weigh WF, the others
-// WS).  The quotients are formed in fp64, where they are exact: the products stay below
-// 2^53 and a quotient that is not an integer lies at least 1 / W(V) >= 2^-16 from one, far
-// more than the rounding of a value below 2^31 (2^-22); an integer division of 64-bit
-// values would cost the combine ~0.8 us and the split kernel its spare scalar registers.
+// The ranges: virtual wave v (of workgroup v >> wl, 2^wl virtual waves per workgroup) starts
+// at unit floor(total * W(v) / W(V)), where W(v) sums the weights of the virtual waves
+// before v, each weighing its workgroup's class weight (F workgroups dispatched first).
+// The quotients are formed in fp64, where they are exact: the products stay below 2^53
+// (total < 2^36, W(V) < 2^15) and a quotient that is not an integer lies at least 1 / W(V)
+// > 2^-15 from one, more than the rounding of a value below 2^36 (2^-17); an integer
+// division of 64-bit values would cost the split kernel its spare scalar registers.  The
+// merge needs none of this: the split kernel records which ranges hold each sequence.
 template <bool FP8>
 struct RangeSplit {
-  static constexpr int64_t WF = RangeWeights<FP8>::kFirst, WS = RangeWeights<FP8>::kSecond;
-  int64_t total, first, nv, wt;
-  NIA_DEVICE RangeSplit(int64_t total_units, const DecodeParams& p)
-      : total(total_units),
-        first((int64_t)p.first_wgs * p.wph),
-        nv((int64_t)p.grid * p.wph),
-        wt(weight_before((int64_t)p.grid * p.wph, (int64_t)p.first_wgs * p.wph)) {}
-  static NIA_DEVICE int64_t weight_before(int64_t v, int64_t first) {
-    return v <= first ? WF * v : WF * first + WS * (v - first);
+  using RW = RangeWeights<FP8>;
+  static constexpr int64_t W1E = RW::kFirstEven, W1O = RW::kFirstOdd;
+  static constexpr int64_t W2E = RW::kSecondEven, W2O = RW::kSecondOdd;
+  // the weight of each virtual wave of workgroup i
+  static NIA_DEVICE int64_t wg_weight(int64_t i, int64_t F) {
+    return i < F ? ((i & 1) ? W1O : W1E) : ((i & 1) ? W2O : W2E);
+  }
+  // the weights of workgroups 0 .. n - 1 (one virtual wave each)
+  static NIA_DEVICE int64_t wg_sum(int64_t n, int64_t F) {
+    const int64_t n1 = n < F ? n : F;
+    int64_t s = W1E * ((n1 + 1) >> 1) + W1O * (n1 >> 1);
+    if (n > F) s += W2E * (((n + 1) >> 1) - ((F + 1) >> 1)) + W2O * ((n >> 1) - (F >> 1));
+    return s;
+  }
+  static NIA_DEVICE int64_t weight_before(int64_t v, int64_t F, int wl) {
+    if constexpr (FP8) return v;  // even ranges
+    const int64_t n = v >> wl, s = v - (n << wl);
+    return (wg_sum(n, F) << wl) + s * wg_weight(n, F);
   }
   static NIA_DEVICE int64_t at(int64_t total, int64_t w, int64_t wt) {
     return (int64_t)((double)total * (double)w / (double)wt);
-  }
-  NIA_DEVICE int64_t weight_before(int64_t v) const { return weight_before(v, first); }
-  NIA_DEVICE int64_t at(int64_t w) const { return at(total, w, wt); }
-  NIA_DEVICE int64_t start(int64_t v) const { return at(weight_before(v)); }
-  // the range holding unit u: the last v with start(v) <= u
-  NIA_DEVICE int64_t holding(int64_t u) const {
-    // the largest W(v) with start(v) <= u
-    const int64_t w = (int64_t)(((double)(u + 1) * (double)wt - 1.0) / (double)total);
-    const int64_t v = w < WF * first ? w / WF : first + (w - WF * first) / WS;
-    return v < nv - 1 ? v : nv - 1;
   }
 };
 
@@ -704,15 +710,23 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   const int hg = p.hg, wph = p.wph;
   const int hig = wave % hg;   // KV head within the group
   const int slice = wave / hg;
-  // the wave's range, [RangeSplit::start(vw), RangeSplit::start(vw + 1)), from the static
-  // pieces (a RangeSplit object here costs the loop ~25 scalar-register spills)
+  // the wave's range, [floor(total W(vw) / W(V)), floor(total W(vw + 1) / W(V)))
   using Split = RangeSplit<FP8>;
+  const int wl = __builtin_ctz(wph);  // wph is 1, 2 or 4
   const int64_t vw = (int64_t)blockIdx.x * wph + slice;
-  const int64_t fv = (int64_t)p.first_wgs * wph;
-  const int64_t wt = Split::weight_before((int64_t)p.grid * wph, fv);
-  const int64_t ustart = Split::at(total, Split::weight_before(vw, fv), wt);
-  const int64_t uend = Split::at(total, Split::weight_before(vw + 1, fv), wt);
-  if (ustart >= uend) return;  // no barrier follows: waves leave on their own
+  const int64_t wt = Split::weight_before((int64_t)p.grid * wph, p.first_wgs, wl);
+  const int64_t ustart = Split::at(total, Split::weight_before(vw, p.first_wgs, wl), wt);
+  const int64_t uend = Split::at(total, Split::weight_before(vw + 1, p.first_wgs, wl), wt);
+  if (ustart >= uend) {
+    // An empty range: the merge of a sequence that spans it reads its slot 0, which says
+    // "no keys" (m = -inf, l = 0; o is not read then).  No barrier follows: waves leave on
+    // their own.
+    if (lane < G && quad == 0) {
+      const int64_t row = ((vw * 2) * hg + hig) * G + lane;
+      *reinterpret_cast<float2*>(p.sp_ml + 2 * row) = make_float2(-INFINITY, 0.f);
+    }
+    return;
+  }
 
   // ---- walking the unit range ----------------------------------------------------------------
   // The unit prefix and the context lengths come from LDS, or for large batches through
@@ -882,6 +896,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     const int hk = x.g * hg + hig;
     const int64_t U0 = x.u - x.j;
     const bool whole = U0 >= ustart && U0 + x.n <= uend;
+    // the ranges that hold the sequence's first and last unit, for the merge (one wave of the
+    // range writes them: its other waves take other KV heads of the same units)
+    if (hig == 0 && lane == 0) {
+      int32_t* rec = p.ws_rec + 2 * ((int64_t)x.g * batch + x.b);
+      if (U0 >= ustart) rec[0] = (int32_t)(2 * vw + (U0 == ustart ? 0 : 1));
+      if (U0 + x.n <= uend) rec[1] = (int32_t)vw;
+    }
     if (hn < G) {
       if (whole) {
         bf16_t* out = reinterpret_cast<bf16_t*>(p.out) + (int64_t)x.b * p.out_b +
@@ -1101,11 +1122,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_prefix_kernel(DecodePar
 }
 
 // Merge the partials of every (sequence, head) whose units were split over several waves'
-// ranges: one wave per pair, lane l owning output dims 2 l, 2 l + 1.  The partial rows of
-// up to kCombineRows ranges are loaded in one round (their (m, l) and the lane's two
-// dims), then merged online (running max, rescaled sums), so a pair costs two rounds of
-// loads after the unit prefix unless its sequence spans more ranges than that.  Pairs of
-// empty sequences get zeros; pairs finished by the split kernel are left alone.
+// ranges: one wave per pair, lane l owning output dims 2 l, 2 l + 1.  The pair's unit
+// prefix entries and the split kernel's record of its first and last range come in one
+// round of loads (no range arithmetic here: the record names them, and the first range's
+// slot); the partial rows of up to kCombineRows ranges then come in one more (their (m, l)
+// and the lane's two dims) and are merged online (running max, rescaled sums).  An empty
+// range inside a sequence wrote m = -inf there and adds nothing.  Pairs of empty
+// sequences get zeros; pairs finished by the split kernel are left alone.
 constexpr int kCombineRows = 16;
 
 template <int D, bool FP8>
@@ -1116,21 +1139,21 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
   // left to itself the compiler loads each parameter on first use, behind the branches, and
   // the short kernel is a chain of such round trips.
   asm volatile("" ::"s"(p.num_heads), "s"(p.group), "s"(p.hg), "s"(p.ws_pfx), "s"(p.out),
-               "s"(p.out_b), "s"(p.out_h), "s"(p.q_group), "s"(p.nhg), "s"(p.first_wgs),
-               "s"(p.wph), "s"(p.grid), "s"(p.sp_ml), "s"(p.sp_o));
+               "s"(p.out_b), "s"(p.out_h), "s"(p.q_group), "s"(p.ws_rec), "s"(p.sp_ml),
+               "s"(p.sp_o));
   const int lane = threadIdx.x & (kWave - 1);
   const int pair = blockIdx.x * (kCombineThreads / kWave) + (threadIdx.x >> 6);
   const int b = pair / p.num_heads;
   const int bl = b < batch ? b : batch - 1;  // the loads stay inside the prefix
-  const int T = p.ws_pfx[batch];
-  const int pb = p.ws_pfx[bl];
-  const int pb1 = p.ws_pfx[bl + 1];
-  asm volatile("" ::"v"(pb), "v"(pb1), "s"(T));
-  if (pair >= batch * p.num_heads) return;
   const int h = pair - b * p.num_heads;
   const int G = p.group;
   const int hk = h / G, gq = h - hk * G;
   const int g = hk / p.hg, hig = hk - g * p.hg;
+  const int pb = p.ws_pfx[bl];
+  const int pb1 = p.ws_pfx[bl + 1];
+  const int2 rec = *reinterpret_cast<const int2*>(p.ws_rec + 2 * ((int64_t)g * batch + bl));
+  asm volatile("" ::"v"(pb), "v"(pb1), "v"(rec.x), "v"(rec.y));
+  if (pair >= batch * p.num_heads) return;
   const int n_units = pb1 - pb;
   const int d0 = 2 * lane;
   const bool has_dims = d0 < D;
@@ -1140,19 +1163,11 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
     if (has_dims) *reinterpret_cast<uint32_t*>(out + d0) = 0u;
     return;
   }
-  const int64_t total = (int64_t)T * p.nhg;
-  const RangeSplit<FP8> split(total, p);
-  const int64_t U0 = (int64_t)g * T + pb, U1 = U0 + n_units;
-  const int64_t f = split.holding(U0), e = split.holding(U1 - 1);
+  // the ranges f .. e that hold the sequence's units (recorded by the split kernel); f's
+  // partial is in the slot it recorded, the later ones start inside the sequence (slot 0)
+  const int f = rec.x >> 1, e = rec.y;
   if (f == e) return;  // one wave had the whole sequence and wrote it
-  const int n = (int)(e - f + 1);
-  // range starts s(v) = floor(total * W(v) / wt), stepped without divisions: W grows by
-  // the range's weight w, so s grows by q_w plus the carry of r_w over wt
-  const int64_t wt = split.wt;
-  const int64_t qa = split.at(split.WF), ra = total * split.WF - qa * wt;
-  const int64_t qb = split.at(split.WS), rb = total * split.WS - qb * wt;
-  int64_t s_next = split.start(f);
-  int64_t rem = total * split.weight_before(f) - s_next * wt;  // (total * W(v)) mod wt
+  const int n = e - f + 1;
   float m_run = -INFINITY, l_run = 0.f;
   float2 acc = make_float2(0.f, 0.f);
   for (int c0 = 0; c0 < n; c0 += kCombineRows) {
@@ -1163,18 +1178,10 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
       o[i] = make_float2(0.f, 0.f);
       const int64_t v = f + c0 + i;
       if (c0 + i < n) {
-        const int64_t s0 = s_next;
-        const bool first = v < split.first;
-        rem += first ? ra : rb;
-        s_next += (first ? qa : qb) + (rem >= wt ? 1 : 0);
-        rem -= rem >= wt ? wt : 0;
-        const int64_t s1 = s_next;
-        if (s0 < s1) {  // an empty range wrote nothing
-          const int sl = U0 <= s0 ? 0 : 1;
-          const int64_t row = ((v * 2 + sl) * p.hg + hig) * G + gq;
-          ml[i] = *reinterpret_cast<const float2*>(p.sp_ml + 2 * row);
-          if (has_dims) o[i] = *reinterpret_cast<const float2*>(p.sp_o + row * D + d0);
-        }
+        const int sl = c0 + i == 0 ? (rec.x & 1) : 0;
+        const int64_t row = ((v * 2 + sl) * p.hg + hig) * G + gq;
+        ml[i] = *reinterpret_cast<const float2*>(p.sp_ml + 2 * row);
+        if (has_dims) o[i] = *reinterpret_cast<const float2*>(p.sp_o + row * D + d0);
       }
     }
     float cm = m_run;
@@ -1204,7 +1211,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_split_combine_kernel(D
 constexpr int kPartBlocks = 32;  // fp32 partition kernel: 512 tokens per partition
 
 // Workspace layout: [header (256 B, reserved; nothing reads or writes it)][per path:
-//   split:  ws_pfx (batch + 1 ints, rounded to 256 B)][sp_ml][sp_o]
+//   split:  ws_pfx (batch + 1 ints, rounded to 256 B)][ws_rec (2 ints per sequence and KV
+//           head group, rounded to 256 B)][sp_ml][sp_o]
 //   fp32 partitions:  [ws_ml][ws_o]]
 constexpr size_t kHeaderBytes = 256;
 
@@ -1216,6 +1224,11 @@ int32_t decode_max_parts(int32_t max_blocks_per_seq) {
 
 size_t split_pfx_bytes(int32_t batch) { return round_up((size_t)(batch + 1) * sizeof(int), 256); }
 
+// The merge's range records, for at most num_kv_heads head groups.
+size_t split_rec_bytes(int32_t batch, int32_t num_kv_heads) {
+  return round_up((size_t)batch * num_kv_heads * 2 * sizeof(int), 256);
+}
+
 // Partial rows of the split kernel: grid * wph ranges x 2 slots x hg heads x G = 8 G per
 // workgroup, for the largest grid.
 size_t split_rows(int32_t group) { return (size_t)kSplitMaxGrid * 8 * (size_t)group; }
@@ -1225,9 +1238,9 @@ size_t split_rows(int32_t group) { return (size_t)kSplitMaxGrid * 8 * (size_t)gr
 // workspace.
 constexpr int kSplitMaxGroup = 16;
 
-size_t split_workspace(int32_t batch, int32_t group, int32_t head_dim) {
+size_t split_workspace(int32_t batch, int32_t num_kv_heads, int32_t group, int32_t head_dim) {
   const int32_t g = group < kSplitMaxGroup ? group : kSplitMaxGroup;
-  return kHeaderBytes + split_pfx_bytes(batch) +
+  return kHeaderBytes + split_pfx_bytes(batch) + split_rec_bytes(batch, num_kv_heads) +
          split_rows(g) * ((size_t)head_dim + 2) * sizeof(float);
 }
 
@@ -1342,7 +1355,7 @@ extern "C" size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_hea
     return kHeaderBytes +
            (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
   }
-  return split_workspace(batch, group, head_dim);
+  return split_workspace(batch, num_kv_heads, group, head_dim);
 }
 
 namespace {
@@ -1468,7 +1481,9 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
   p.wph = 4 / p.hg;
   p.nhg = num_kv_heads / p.hg;
   p.ws_pfx = reinterpret_cast<int32_t*>(ws + kHeaderBytes);
-  p.sp_ml = reinterpret_cast<float*>(ws + kHeaderBytes + split_pfx_bytes(batch));
+  p.ws_rec = reinterpret_cast<int32_t*>(ws + kHeaderBytes + split_pfx_bytes(batch));
+  p.sp_ml = reinterpret_cast<float*>(ws + kHeaderBytes + split_pfx_bytes(batch) +
+                                     split_rec_bytes(batch, num_kv_heads));
   p.sp_o = p.sp_ml + split_rows(G < kSplitMaxGroup ? G : kSplitMaxGroup) * 2;
   p.q_group = G;
   // query heads kSplitMaxGroup * c .. of every KV head group in launch c
