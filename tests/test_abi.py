@@ -100,13 +100,18 @@ def test_noalloc_decode_refuses_sizes_beyond_its_scratch_without_launching():
 def test_workspace_size():
     lib = _lib.load()
     hdr = 256
-    # bf16 (and fp8): the unit prefix (batch + 1 ints, rounded to 256 B), then (m, l) and
-    # the partial output of 8 G rows per workgroup for a grid of at most 512
+    # bf16 (and fp8): the unit prefix (batch + 1 ints, rounded to 256 B), the merge's range
+    # records (2 ints per sequence and KV head, rounded to 256 B), then (m, l) and the
+    # partial output of 8 G rows per workgroup for a grid of at most 512
     pfx = -(-(64 + 1) * 4 // 256) * 256
+    rec = -(-(64 * 8 * 2 * 4) // 256) * 256
     assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, 16, 128, 0) == \
-        hdr + pfx + 512 * 8 * 4 * 130 * 4
+        hdr + pfx + rec + 512 * 8 * 4 * 130 * 4
     assert lib.nia_paged_decode_workspace_size(64, 32, 8, 32, 16, 80, 0) == \
-        hdr + pfx + 512 * 8 * 4 * 82 * 4
+        hdr + pfx + rec + 512 * 8 * 4 * 82 * 4
+    rec3 = -(-(5 * 3 * 2 * 4) // 256) * 256
+    assert lib.nia_paged_decode_workspace_size(5, 6, 3, 32, 16, 128, 0) == \
+        hdr + 256 + rec3 + 512 * 8 * 2 * 130 * 4
     # fp32 at head_dim 128 / block 16: partitions of 32 blocks per (sequence, head)
     assert lib.nia_paged_decode_workspace_size(64, 32, 8, 32, 16, 128, 1) == \
         hdr + 64 * 32 * 130 * 4
