@@ -124,6 +124,16 @@ def test_bf16_one_long_sequence_over_many_ranges(batch):
     assert_attn_close(step(c), oracle(c), torch.bfloat16, f"64k context, batch {batch}")
 
 
+@pytest.mark.parametrize("hkv,lens", [(8, [1000, 37]), (1, [3000, 1, 5]), (2, [64, 33, 1, 500])])
+def test_bf16_fewer_units_than_ranges(hkv, lens):
+    """Fewer 32-key units than the grid has ranges: most ranges are empty, and a sequence's
+    units lie in ranges with empty ones between them, whose slots the merge reads as "no
+    keys"; the merge takes the first and last range from the split kernel's records."""
+    c = workloads.make_decode(len(lens), 2 * hkv, hkv, 128, lens, 400, 16, torch.bfloat16,
+                              "cuda", seed=1235 + hkv)
+    assert_attn_close(step(c), oracle(c), torch.bfloat16, f"few units, H_kv {hkv}")
+
+
 def test_bf16_batch_beyond_the_lds_prefix():
     """3000 sequences: the unit prefix is built by its own kernel; many sequences per
     range (checked on a sample of 60)."""
