@@ -1385,28 +1385,38 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
   if (dtype != NIA_DTYPE_BF16 && (fp8 || dtype != NIA_DTYPE_F32)) return NIA_ERR_UNSUPPORTED;
   const int G = num_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NIA_DTYPE_BF16 && !split_shape(fp8, head_dim, block_size, G))
-    return NIA_ERR_UNSUPPORTED;
-
-  if (dtype == NIA_DTYPE_F32 && !f32_partition_shape(head_dim, block_size, G)) {
-    // other fp32 shapes: the fp32 prefill kernel with one query row per sequence (any block
-    // size, head_dim 64 / 80 / 96 / 128, any group)
+  const bool generic = dtype == NIA_DTYPE_F32 ? !f32_partition_shape(head_dim, block_size, G)
+                                              : !split_shape(fp8, head_dim, block_size, G);
+  if (generic) {
+    // Shapes the tuned kernels do not take (fp32 beyond the partition kernel's; bf16 and fp8
+    // block sizes that are not powers of two, or below 4 / 16): the fp32 prefill kernel with
+    // one query row per sequence and bottom-right masking, which maps every key through the
+    // table on its own (any block size, head_dim 64 / 80 / 96 / 128 (fp8: 128), any group).
     if (head_dim != 64 && head_dim != 80 && head_dim != 96 && head_dim != 128)
       return NIA_ERR_UNSUPPORTED;
-    if (block_size <= 0) return NIA_ERR_UNSUPPORTED;
-    if ((uintptr_t)q % 16 || q_batch_stride % 4 || q_head_stride % 4 || (uintptr_t)out % 16 ||
-        out_batch_stride % 4 || out_head_stride % 4 || (uintptr_t)k_cache % 16 ||
-        (uintptr_t)v_cache % 16)
+    if (fp8 && head_dim != 128) return NIA_ERR_UNSUPPORTED;
+    if (block_size <= 0 || (int64_t)max_blocks_per_seq * block_size > INT32_MAX)
+      return NIA_ERR_UNSUPPORTED;
+    const int elem = dtype == NIA_DTYPE_F32 ? kElemF32 : (fp8 ? kElemFp8 : kElemBf16);
+    // q / out: 16 bytes (fp32) or 8 bytes (bf16) per lane access of four elements; cache
+    // rows: the same for fp32 / bf16, 4 bytes of fp8 codes
+    const unsigned qa = elem == kElemF32 ? 16u : 8u;
+    const unsigned ca = elem == kElemF32 ? 16u : (elem == kElemBf16 ? 8u : 4u);
+    if ((uintptr_t)q % qa || q_batch_stride % 4 || q_head_stride % 4 || (uintptr_t)out % qa ||
+        out_batch_stride % 4 || out_head_stride % 4 || (uintptr_t)k_cache % ca ||
+        (uintptr_t)v_cache % ca || (fp8 && ((uintptr_t)k_scale % 16 || (uintptr_t)v_scale % 16)))
       return NIA_ERR_MISALIGNED;
     PrefillF32Params f{};
-    f.o = (float*)out;
+    f.o = out;
     f.o_tok = out_batch_stride;
     f.o_head = out_head_stride;
-    f.q = (const float*)q;
+    f.q = q;
     f.q_tok = q_batch_stride;
     f.q_head = q_head_stride;
-    f.k = (const float*)k_cache;
-    f.v = (const float*)v_cache;
+    f.k = k_cache;
+    f.v = v_cache;
+    f.k_scale = fp8 ? k_scale : nullptr;
+    f.v_scale = fp8 ? v_scale : nullptr;
     f.ctx_len = context_lens;
     f.block_tables = block_tables;
     f.bt_stride = bt_stride;
@@ -1419,7 +1429,7 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
     f.causal = NIA_CAUSAL_BOTTOM_RIGHT;
     f.decode = 1;
     f.scale_log2 = (double)scale * 1.4426950408889634;
-    return launch_prefill_f32(f, true, head_dim, batch, 1, s);
+    return launch_prefill_f32(f, true, head_dim, batch, 1, s, elem);
   }
 
   DecodeParams p{};

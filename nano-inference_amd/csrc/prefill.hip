@@ -1252,21 +1252,30 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
   if (max_blocks_per_seq > 0 && (!k_cache || !v_cache || !block_tables))
     return NIA_ERR_INVALID_ARGUMENT;
   if (!supported_head_dim(head_dim) || block_size <= 0) return NIA_ERR_UNSUPPORTED;
-  if (dtype == NIA_DTYPE_F32) {
-    // any block size: the fp32 kernel maps every key through the table on its own
-    if (!vec_ok_f32(q, q_tok_stride, q_head_stride) ||
-        !vec_ok_f32(out, out_tok_stride, out_head_stride) || (uintptr_t)k_cache % 16 ||
-        (uintptr_t)v_cache % 16)
+  // the key positions of a sequence (table width x block size) must fit an int
+  if ((int64_t)max_blocks_per_seq * block_size > INT32_MAX) return NIA_ERR_UNSUPPORTED;
+  if (dtype != NIA_DTYPE_F32 && dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
+  if (dtype == NIA_DTYPE_F32 || (block_size & (block_size - 1))) {
+    // fp32, and bf16 block sizes that are not powers of two (the bf16 kernel finds a row's
+    // block and slot with a shift and a mask): the fp32 kernel, which maps every key through
+    // the table on its own (any block size), reading bf16 rows where the cache holds them
+    const bool f32 = dtype == NIA_DTYPE_F32;
+    if (f32 ? (!vec_ok_f32(q, q_tok_stride, q_head_stride) ||
+               !vec_ok_f32(out, out_tok_stride, out_head_stride) || (uintptr_t)k_cache % 16 ||
+               (uintptr_t)v_cache % 16)
+            : ((uintptr_t)q % 8 || q_tok_stride % 4 || q_head_stride % 4 || (uintptr_t)out % 8 ||
+               out_tok_stride % 4 || out_head_stride % 4 || (uintptr_t)k_cache % 8 ||
+               (uintptr_t)v_cache % 8))
       return NIA_ERR_MISALIGNED;
     PrefillF32Params f{};
-    f.o = (float*)out;
+    f.o = out;
     f.o_tok = out_tok_stride;
     f.o_head = out_head_stride;
-    f.q = (const float*)q;
+    f.q = q;
     f.q_tok = q_tok_stride;
     f.q_head = q_head_stride;
-    f.k = (const float*)k_cache;
-    f.v = (const float*)v_cache;
+    f.k = k_cache;
+    f.v = v_cache;
     f.q_start = q_start;
     f.q_len = q_len;
     f.ctx_len = context_lens;
@@ -1280,13 +1289,10 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
     f.group = num_heads / num_kv_heads;
     f.causal = causal;
     f.scale_log2 = (double)scale * 1.4426950408889634;
-    return launch_prefill_f32(f, true, head_dim, num_seqs, max_q_len, (hipStream_t)stream);
+    return launch_prefill_f32(f, true, head_dim, num_seqs, max_q_len, (hipStream_t)stream,
+                              f32 ? kElemF32 : kElemBf16);
   }
-  if (dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
-  // Power-of-two block sizes: a row's block and slot are a shift and a mask.  The key
-  // positions of a sequence (table width x block size) must fit an int.
-  if (block_size & (block_size - 1)) return NIA_ERR_UNSUPPORTED;
-  if ((int64_t)max_blocks_per_seq * block_size > INT32_MAX) return NIA_ERR_UNSUPPORTED;
+  // bf16, power-of-two block sizes: a row's block and slot are a shift and a mask
   if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride) ||
       (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
     return NIA_ERR_MISALIGNED;

@@ -5,15 +5,21 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Element kinds of q / K / V / o (launch_prefill_f32's `elem`): fp32 throughout; bf16
+// throughout (paged caches); a paged fp8 cache (e4m3 codes, fp32 row scales) with bf16 q / o.
+constexpr int kElemF32 = 0, kElemBf16 = 1, kElemFp8 = 2;
+
 struct PrefillF32Params {
-  float* o;
+  void* o;
   int64_t o_tok, o_head;
-  const float* q;
+  const void* q;
   int64_t q_tok, q_head;
-  const float* k;  // contiguous K/V rows, or the paged cache slice [NB, H_kv, BS, D]
+  const void* k;  // contiguous K/V rows, or the paged cache slice [NB, H_kv, BS, D]
   int64_t k_tok, k_head;
-  const float* v;
+  const void* v;
   int64_t v_tok, v_head;
+  const float* k_scale;  // fp8 caches: [NB, H_kv, BS] row scales
+  const float* v_scale;
   const int32_t* q_start;
   const int32_t* q_len;
   const int32_t* k_start;  // contiguous mode
@@ -36,6 +42,7 @@ struct PrefillF32Params {
   int64_t bias_seq, bias_head, bias_q;
 };
 
-// Grid (m-blocks of 64 rows, heads, sequences); returns an NIA_* status.
+// Grid (m-blocks of 64 rows, heads, sequences); returns an NIA_* status.  `elem` other
+// than kElemF32 takes a paged cache (fp8: head_dim 128, both scale arrays).
 int32_t launch_prefill_f32(const PrefillF32Params& p, bool paged, int head_dim, int num_seqs,
-                           int max_q_len, hipStream_t stream);
+                           int max_q_len, hipStream_t stream, int elem = kElemF32);

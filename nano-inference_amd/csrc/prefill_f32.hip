@@ -5,6 +5,10 @@
 // 281-284 with scaled_dot_product_attention (:12-50), the vision tower's per-chunk loop
 // (src/nano_inference/layers/vision.py:190-208), and chunked prefill over the paged cache.
 // Same varlen description and causal modes as the bf16 kernels (include/nia_attn.h).
+// The same kernel reads bf16 and fp8 paged caches whose block size the bf16 / fp8 kernels
+// do not take (they find a key's block with a shift; the reference's block size is any
+// positive integer, src/nano_inference/core/config.py:54): decode (one query row per
+// sequence, src/nano_inference/layers/attention.py:285-332) and bf16 chunked prefill.
 //
 // Precision: every score q . k is summed on the fp64 matrix cores
 // (v_mfma_f64_16x16x4_f64, fp32 inputs widened exactly), so it carries no accumulated
@@ -37,9 +41,14 @@ constexpr int kF32BlockN = 32;              // keys per LDS tile
 
 typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
-template <int D, bool PAGED>
+// Element kinds: fp32 rows, bf16 rows, or a paged fp8 cache (e4m3 codes with one fp32
+// scale per cache row; q and o in bf16).  Every element is widened to fp32 in LDS (fp8 as
+// code * row scale in fp32, the rows the fp8 format stands for), so one kernel serves the
+// cache layouts the bf16 and fp8 kernels do not take: any block size, any group.
+template <int D, bool PAGED, int E>
 __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Params p) {
   static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
+  static_assert(E == kElemF32 || PAGED, "bf16 and fp8 elements come from a paged cache");
   constexpr int kRow = D + 4;  // LDS row stride in floats
   constexpr int kC4 = D / 4;   // float4 per row
   __shared__ __attribute__((aligned(16))) float sk[kF32BlockN * kRow];
@@ -83,12 +92,20 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
   // B operand of S^T: q[r][16 c + 4 slot + i] widened to fp64
   double qd[D / 4];
   {
-    const float* qp = p.q + (qstart + (int64_t)(row_ok ? r : 0)) * p.q_tok +
-                      (int64_t)h * p.q_head;
+    const int64_t qrow = (qstart + (int64_t)(row_ok ? r : 0)) * p.q_tok + (int64_t)h * p.q_head;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
-      const float4 u = row_ok ? *reinterpret_cast<const float4*>(qp + 16 * c + 4 * slot)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 u = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row_ok) {
+        if constexpr (E == kElemF32) {
+          u = *reinterpret_cast<const float4*>(static_cast<const float*>(p.q) + qrow + 16 * c +
+                                               4 * slot);
+        } else {
+          const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(p.q) + qrow +
+                                                          16 * c + 4 * slot);
+          u = make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+        }
+      }
       qd[4 * c + 0] = u.x;
       qd[4 * c + 1] = u.y;
       qd[4 * c + 2] = u.z;
@@ -116,21 +133,41 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
       float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
       bool ok = t < klen;
       if (ok) {
-        const float *kr, *vr;
+        int64_t kr, vr;  // element offsets of the key's K and V rows
         if constexpr (PAGED) {
           const int blk = bt[t / p.block_size];
           ok = blk >= 0 && (int64_t)blk < p.num_blocks;
-          const int64_t row =
-              (((int64_t)(ok ? blk : 0) * p.num_kv_heads + hk) * p.block_size + t % p.block_size) * D;
-          kr = p.k + row;
-          vr = p.v + row;
+          kr = vr = ((int64_t)(ok ? blk : 0) * p.num_kv_heads + hk) * p.block_size +
+                    t % p.block_size;  // the cache row; elements below
         } else {
-          kr = p.k + (kstart + t) * p.k_tok + (int64_t)hk * p.k_head;
-          vr = p.v + (kstart + t) * p.v_tok + (int64_t)hk * p.v_head;
+          kr = (kstart + t) * p.k_tok + (int64_t)hk * p.k_head;
+          vr = (kstart + t) * p.v_tok + (int64_t)hk * p.v_head;
         }
         if (ok) {
-          kv = *reinterpret_cast<const float4*>(kr + 4 * c4);
-          vv = *reinterpret_cast<const float4*>(vr + 4 * c4);
+          if constexpr (E == kElemF32) {
+            const int64_t m = PAGED ? D : 1;
+            kv = *reinterpret_cast<const float4*>(static_cast<const float*>(p.k) + kr * m + 4 * c4);
+            vv = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v) + vr * m + 4 * c4);
+          } else if constexpr (E == kElemBf16) {
+            const uint2 a = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(p.k) +
+                                                            kr * D + 4 * c4);
+            const uint2 b = *reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(p.v) +
+                                                            vr * D + 4 * c4);
+            kv = make_float4(bf16_lo(a.x), bf16_hi(a.x), bf16_lo(a.y), bf16_hi(a.y));
+            vv = make_float4(bf16_lo(b.x), bf16_hi(b.x), bf16_lo(b.y), bf16_hi(b.y));
+          } else {
+            const uint32_t a = *reinterpret_cast<const uint32_t*>(
+                static_cast<const uint8_t*>(p.k) + kr * D + 4 * c4);
+            const uint32_t b = *reinterpret_cast<const uint32_t*>(
+                static_cast<const uint8_t*>(p.v) + vr * D + 4 * c4);
+            const float ks = p.k_scale[kr], vs = p.v_scale[vr];
+            const uint32_t a0 = bf16x2_from_fp8x2<false>(a), a1 = bf16x2_from_fp8x2<true>(a);
+            const uint32_t b0 = bf16x2_from_fp8x2<false>(b), b1 = bf16x2_from_fp8x2<true>(b);
+            kv = make_float4(bf16_lo(a0) * ks, bf16_hi(a0) * ks, bf16_lo(a1) * ks,
+                             bf16_hi(a1) * ks);
+            vv = make_float4(bf16_lo(b0) * vs, bf16_hi(b0) * vs, bf16_lo(b1) * vs,
+                             bf16_hi(b1) * vs);
+          }
         }
       }
       *reinterpret_cast<float4*>(sk + key * kRow + 4 * c4) = kv;
@@ -204,26 +241,43 @@ __global__ __launch_bounds__(kF32Threads) void prefill_f32_kernel(PrefillF32Para
   l_run += __shfl_xor(l_run, 32, kWave);
   if (!row_ok) return;
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  float* op = p.o + (qstart + (int64_t)r) * p.o_tok + (int64_t)h * p.o_head;
+  const int64_t orow = (qstart + (int64_t)r) * p.o_tok + (int64_t)h * p.o_head;
 #pragma unroll
-  for (int t = 0; t < D / 16; ++t)
-    *reinterpret_cast<float4*>(op + 16 * t + 4 * slot) =
-        make_float4(oacc[t][0] * inv, oacc[t][1] * inv, oacc[t][2] * inv, oacc[t][3] * inv);
+  for (int t = 0; t < D / 16; ++t) {
+    if constexpr (E == kElemF32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(p.o) + orow + 16 * t + 4 * slot) =
+          make_float4(oacc[t][0] * inv, oacc[t][1] * inv, oacc[t][2] * inv, oacc[t][3] * inv);
+    } else {
+      *reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.o) + orow + 16 * t + 4 * slot) =
+          make_uint2(pack_bf16x2(oacc[t][0] * inv, oacc[t][1] * inv),
+                     pack_bf16x2(oacc[t][2] * inv, oacc[t][3] * inv));
+    }
+  }
 }
 
 }  // namespace
 
 int32_t launch_prefill_f32(const PrefillF32Params& p, bool paged, int head_dim, int num_seqs,
-                           int max_q_len, hipStream_t stream) {
+                           int max_q_len, hipStream_t stream, int elem) {
   if (num_seqs > 65535 || p.num_heads > 65535) return NIA_ERR_UNSUPPORTED;
+  if (elem != kElemF32 && (!paged || elem != kElemBf16) && (!paged || elem != kElemFp8))
+    return NIA_ERR_UNSUPPORTED;
+  if (elem == kElemFp8 && (head_dim != 128 || !p.k_scale || !p.v_scale))
+    return NIA_ERR_UNSUPPORTED;
   const dim3 grid((max_q_len + kF32BlockM - 1) / kF32BlockM, p.num_heads, num_seqs);
+  if (elem == kElemFp8) {
+    nia_launch((prefill_f32_kernel<128, true, kElemFp8>), grid, dim3(kF32Threads), stream, p);
+    return hipGetLastError() == hipSuccess ? NIA_OK : NIA_ERR_LAUNCH;
+  }
   switch (head_dim) {
 #define NIA_F32_CASE(DD)                                                                      \
   case DD:                                                                                    \
-    if (paged)                                                                                \
-      nia_launch((prefill_f32_kernel<DD, true>), grid, dim3(kF32Threads), stream, p);         \
+    if (!paged)                                                                               \
+      nia_launch((prefill_f32_kernel<DD, false, kElemF32>), grid, dim3(kF32Threads), stream, p); \
+    else if (elem == kElemF32)                                                                \
+      nia_launch((prefill_f32_kernel<DD, true, kElemF32>), grid, dim3(kF32Threads), stream, p); \
     else                                                                                      \
-      nia_launch((prefill_f32_kernel<DD, false>), grid, dim3(kF32Threads), stream, p);        \
+      nia_launch((prefill_f32_kernel<DD, true, kElemBf16>), grid, dim3(kF32Threads), stream, p); \
     break;
     NIA_F32_CASE(64)
     NIA_F32_CASE(80)

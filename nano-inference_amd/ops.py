@@ -206,14 +206,14 @@ def check_pool_shape(head_dim: int, block_size: int, num_heads: int, num_kv_head
     limits of include/nia_attn.h), so that a pool can be checked when it is built, before
     any step runs:
 
-    * bf16 caches: block size a power of two >= 4 (decode; chunked prefill takes any
-      power of two, the KV writes any size), head_dim 64 / 80 / 96 / 128, any group;
-    * fp8 caches: head_dim 128, block size a power of two >= 16;
-    * fp32 caches: head_dim 64 / 80 / 96 / 128, any block size and group.
+    * bf16 and fp32 caches: head_dim 64 / 80 / 96 / 128, any block size and group;
+    * fp8 caches: head_dim 128, any block size and group.
 
-    Block sizes that are not powers of two are refused for bf16 and fp8 caches: the
-    kernels find a key's block and slot with a shift and a mask (the reference's block
-    size is a free integer, src/nano_inference/core/config.py:54; 16 is its default)."""
+    Any positive block size is taken, as the reference's (a free integer,
+    src/nano_inference/core/config.py:54; 16 is its default).  The tuned bf16 / fp8 kernels
+    find a key's block and slot with a shift and a mask: bf16 block sizes that are powers of
+    two >= 4 (fp8: >= 16) run them, other sizes run the fp32-softmax kernel that maps every
+    key through the table on its own (correct, several times slower)."""
     if num_kv_heads <= 0 or num_heads <= 0 or num_heads % num_kv_heads != 0:
         raise ValueError(f"num_heads must be divisible by num_kv_heads, got {num_heads=} and "
                          f"{num_kv_heads=}")
@@ -221,16 +221,8 @@ def check_pool_shape(head_dim: int, block_size: int, num_heads: int, num_kv_head
         raise ValueError(f"paged attention supports head_dim 64, 80, 96 or 128, not {head_dim}")
     if block_size <= 0:
         raise ValueError(f"block_size must be positive, got {block_size}")
-    if dtype == torch.float32 and not fp8_cache:
-        return
-    pow2 = block_size & (block_size - 1) == 0
-    if fp8_cache:
-        if head_dim != 128 or not pow2 or block_size < 16:
-            raise ValueError("fp8 KV caches need head_dim 128 and a power-of-two block size "
-                             f">= 16 (got head_dim {head_dim}, block_size {block_size})")
-    elif not pow2 or block_size < 4:
-        raise ValueError("bf16 KV caches need a power-of-two block size >= 4, "
-                         f"got {block_size}")
+    if fp8_cache and head_dim != 128:
+        raise ValueError(f"fp8 KV caches need head_dim 128 (got head_dim {head_dim})")
 
 
 def check_decode_shape(head_dim: int, block_size: int, num_heads: int, num_kv_heads: int,

@@ -52,11 +52,17 @@ def test_validation_returns_codes_without_launching():
     # decode: heads not divisible
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 6, 4, 128, 16, 10, 0.1,
                                 None, 0, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    # decode: unsupported head_dim; bf16 block size 2
+    # decode: unsupported head_dim, also at a block size the split kernels do not take
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 72, 16, 10, 0.1,
                                 None, 0, 0, None) == _lib.ERR_UNSUPPORTED
-    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 128, 2, 10, 0.1,
-                                p, 1 << 30, 0, None) == _lib.ERR_UNSUPPORTED
+    assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 72, 12, 10, 0.1,
+                                None, 0, 0, None) == _lib.ERR_UNSUPPORTED
+    # bf16 block sizes 2 and 12 take the any-size kernel, whose checks see a q that is not
+    # 8-byte aligned
+    odd = ctypes.c_void_p(18)
+    for bs in (2, 12):
+        assert lib.nia_paged_decode(p, 0, 0, odd, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 128, bs, 10,
+                                    0.1, p, 1 << 30, 0, None) == _lib.ERR_MISALIGNED
     # a group of 32 is a supported shape: validation gets as far as the workspace alignment
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 32, 1, 128, 16, 10, 0.1,
                                 p, 1 << 30, 0, None) == _lib.ERR_MISALIGNED
@@ -78,8 +84,11 @@ def test_validation_returns_codes_without_launching():
                            5, 0, None) == _lib.ERR_INVALID_ARGUMENT
     assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.0,
                            1, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    # paged prefill: block size not a power of two
-    assert lib.nia_prefill_paged(p, 8, 8, p, 8, 8, p, p, p, 4, 4, p, p, p, 1, 4, 2, 2, 128, 12,
+    # paged prefill: a bf16 block size that is not a power of two takes the any-size
+    # kernel (its checks see the unaligned q); an unsupported head_dim is refused first
+    assert lib.nia_prefill_paged(p, 8, 8, ctypes.c_void_p(18), 8, 8, p, p, p, 4, 4, p, p, p, 1,
+                                 4, 2, 2, 128, 12, 10, 0.1, 2, 0, None) == _lib.ERR_MISALIGNED
+    assert lib.nia_prefill_paged(p, 8, 8, p, 8, 8, p, p, p, 4, 4, p, p, p, 1, 4, 2, 2, 72, 12,
                                  10, 0.1, 2, 0, None) == _lib.ERR_UNSUPPORTED
 
 

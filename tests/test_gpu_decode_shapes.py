@@ -1,5 +1,6 @@
 """Paged decode over the layouts the reference's configuration allows: block sizes other
-than 16 (src/nano_inference/core/config.py:54 makes it a setting), head dims 64 / 80 / 96,
+than 16, powers of two or not (src/nano_inference/core/config.py:54 makes it a setting),
+head dims 64 / 80 / 96,
 any group (more than 16 query heads per KV head run as launches of at most 16 heads
 each), KV head counts whose groups of the split kernel take 1, 2 or 4 heads per
 workgroup, batches beyond the in-LDS unit prefix, and pools with invalid block ids.
@@ -63,6 +64,21 @@ def test_bf16_block_sizes(bs):
     c = workloads.make_decode(len(lens), 16, 4, 128, lens, sum(-(-L // bs) for L in lens) + 9, bs,
                               torch.bfloat16, "cuda", seed=1200 + bs)
     assert_attn_close(step(c), oracle(c), torch.bfloat16, f"bf16 block size {bs}")
+
+
+@pytest.mark.parametrize("bs,head_dim,hkv,group", [(12, 128, 4, 4), (24, 128, 2, 7),
+                                                   (48, 80, 2, 2), (5, 64, 1, 3),
+                                                   (2, 96, 2, 20), (1, 128, 8, 1),
+                                                   (100, 128, 1, 16)])
+def test_bf16_block_sizes_not_powers_of_two(bs, head_dim, hkv, group):
+    """Block sizes the split kernels do not take (not powers of two, or below 4; the
+    reference's is any positive integer): the any-size kernel over the bf16 rows, at
+    several head dims and groups (20 beyond the split kernels' 16 MFMA columns)."""
+    lens = edge_lens(bs)
+    c = workloads.make_decode(len(lens), hkv * group, hkv, head_dim, lens,
+                              sum(-(-L // bs) for L in lens) + 9, bs, torch.bfloat16, "cuda",
+                              seed=1290 + bs + head_dim)
+    assert_attn_close(step(c), oracle(c), torch.bfloat16, f"bf16 bs={bs} D={head_dim} G={group}")
 
 
 @pytest.mark.parametrize("head_dim", [64, 80, 96])
@@ -176,8 +192,10 @@ def test_bf16_invalid_block_ids_are_skipped():
         assert_attn_close(out, exp, torch.bfloat16, f"invalid ids bs={bs}")
 
 
-@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("bs", [32, 64, 8, 12, 24, 1])
 def test_fp8_block_sizes(bs):
+    """fp8 caches at block sizes 32 and 64 (split kernels) and 8, 12, 24, 1 (the any-size
+    kernel, rows dequantised on load)."""
     from tests.test_gpu_fp8_kv import oracle_decode_fp8
     lens = edge_lens(bs)
     c = workloads.make_decode(len(lens), 16, 4, 128, lens, sum(-(-L // bs) for L in lens) + 9, bs,
@@ -204,8 +222,9 @@ def test_fp32_other_layouts(head_dim, bs, hkv, group):
 
 
 def test_unsupported_layouts_raise_before_launch():
-    c = workloads.make_decode(2, 8, 2, 128, [5, 9], 8, 2, torch.bfloat16, "cuda", seed=1280)
-    with pytest.raises(ValueError, match="block size"):
+    c = workloads.make_decode(2, 8, 2, 112, [5, 9], 8, 16, torch.bfloat16, "cuda", seed=1280)
+    with pytest.raises(ValueError, match="head_dim"):
         ops.paged_decode(c.q, c.k_cache[0], c.v_cache[0], c.block_tables, c.context_lens)
     ops.check_decode_shape(128, 16, 32, 1)  # any group
-    ops.check_decode_shape(128, 2, 32, 1, torch.float32)  # fp32 takes any layout
+    ops.check_decode_shape(128, 2, 32, 1)  # any block size
+    ops.check_decode_shape(128, 2, 32, 1, torch.float32)

@@ -223,6 +223,22 @@ def test_chunked_prefill_block_sizes_full(bs):
         assert_attn_close(o[s * c.chunk + idx], ref, torch.bfloat16, f"bs {bs} chunk {s}")
 
 
+@pytest.mark.parametrize("bs,group", [(1, 4), (5, 4), (12, 4), (24, 7), (100, 2)])
+def test_chunked_prefill_other_block_sizes_full(bs, group):
+    """Block sizes that are not powers of two (the reference's block size is any positive
+    integer, src/nano_inference/core/config.py:54), which the any-size kernel takes over
+    the bf16 rows: prior lengths on both sides of block edges, every row checked."""
+    prior = [0, 1, max(bs - 1, 0), bs, bs + 1, 3 * bs + 7]
+    c = workloads.chunked_qwen3_8b("cuda", n=6, chunk=80, prior=prior, num_heads=2 * group,
+                                   num_kv_heads=2, block_size=bs)
+    out = ops.prefill_paged(c.q, c.k_cache, c.v_cache, c.block_tables, c.q_start, c.q_len,
+                            c.context_lens, c.chunk)
+    torch.cuda.synchronize()
+    o = out.double().cpu().numpy()
+    for s, (idx, ref) in _chunk_oracle(c, None).items():
+        assert_attn_close(o[s * c.chunk + idx], ref, torch.bfloat16, f"bs {bs} chunk {s}")
+
+
 def test_chunk_rows_equal_full_prefill_rows():
     """A chunk at positions P.. of a sequence equals those rows of the full causal prefill."""
     n, p_len, chunk, bs = 1, 700, 300, 16
