@@ -102,7 +102,8 @@ int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
  *     two >= 4 run the key-range split kernels (groups of more than 16 query heads per
  *     KV head as several launches of at most 16 heads each, which share the workspace
  *     one after another on the stream); other block sizes run the kernel of the f32
- *     path below over bf16 rows (q . k in fp64; several times slower), with
+ *     path below over bf16 rows (q . k in fp64; several times slower; no partials,
+ *     so the workspace size is the 256-byte header), with
  *     max_blocks_per_seq * block_size < 2^31;
  *   dtype f32 (q . k summed in fp64): any block_size, head_dim 64, 80, 96 or 128, any
  *     num_heads / num_kv_heads.

@@ -1355,6 +1355,10 @@ extern "C" size_t nia_paged_decode_workspace_size(int32_t batch, int32_t num_hea
     return kHeaderBytes +
            (size_t)batch * num_heads * parts * ((size_t)head_dim + 2) * sizeof(float);
   }
+  // Block sizes the split kernels do not take run the any-size kernel, which needs no
+  // workspace (fp8 caches take the split kernels at a subset of the bf16 shapes, so a
+  // bf16 query never reports less than an fp8 call needs).
+  if (!split_shape(false, head_dim, block_size, group)) return kHeaderBytes;
   return split_workspace(batch, num_kv_heads, group, head_dim);
 }
 

@@ -128,6 +128,10 @@ def test_workspace_size():
         hdr + 64 * 32 * 16 * 130 * 4
     # fp32 other shapes run without partials
     assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, 32, 128, 1) == hdr
+    # bf16 block sizes the split kernels do not take run the any-size kernel, without
+    # partials either
+    for bs in (1, 2, 12, 24, 48):
+        assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, bs, 128, 0) == hdr
     assert lib.nia_paged_decode_workspace_size(64, 32, 3, 512, 16, 128, 0) == 0  # 32 % 3
 
 
