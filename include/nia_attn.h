@@ -98,13 +98,13 @@ int32_t nia_kv_write(const void* k, int64_t k_tok_stride, int64_t k_head_stride,
  * Supported:
  *   dtype bf16 (fp32 softmax and accumulation): any block_size >= 1 (the reference's
  *     block size is a free integer, src/nano_inference/core/config.py:54), head_dim
- *     64, 80, 96 or 128, any num_heads / num_kv_heads.  Block sizes that are powers of
- *     two >= 4 run the key-range split kernels (groups of more than 16 query heads per
- *     KV head as several launches of at most 16 heads each, which share the workspace
- *     one after another on the stream); other block sizes run the kernel of the f32
- *     path below over bf16 rows (q . k in fp64; several times slower; no partials,
- *     so the workspace size is the 256-byte header), with
- *     max_blocks_per_seq * block_size < 2^31;
+ *     64, 80, 96 or 128, any num_heads / num_kv_heads, max_blocks_per_seq * block_size
+ *     < 2^31.  Block sizes that are multiples of 4 run the key-range split kernels
+ *     (groups of more than 16 query heads per KV head as several launches of at most 16
+ *     heads each, which share the workspace one after another on the stream); other
+ *     block sizes run the kernel of the f32 path below over bf16 rows (q . k in fp64;
+ *     ~25x slower on the Qwen3-8B decode; no partials, so the workspace size is the
+ *     256-byte header);
  *   dtype f32 (q . k summed in fp64): any block_size, head_dim 64, 80, 96 or 128, any
  *     num_heads / num_kv_heads.
  */
@@ -214,10 +214,10 @@ int32_t nia_prefill_masked(void* out, int64_t out_tok_stride, int64_t out_head_s
  * NIA_CAUSAL_BOTTOM_RIGHT; NIA_CAUSAL_NONE lets every row see the whole context.
  * Supported: head_dim 64, 80, 96 or 128; dtype bf16 or f32 with any block_size >= 1
  * and max_blocks_per_seq * block_size < 2^31 (keys in blocks outside [0, num_blocks)
- * are skipped).  bf16 block sizes that are powers of two run the MFMA kernel (16 and
- * more stream 16-row groups of a block into LDS by DMA, smaller ones take
- * register-staged loads); other bf16 block sizes, and f32, run the f32 kernel (q . k in
- * fp64, bf16 rows widened on load; several times slower).
+ * are skipped).  bf16 block sizes >= 2 run the MFMA kernels (multiples of 16 stream
+ * 16-row groups of a block into LDS by DMA, other sizes take register-staged loads,
+ * ~2.5x slower); bf16 block size 1, and f32, run the f32 kernel (q . k in fp64, bf16
+ * rows widened on load).
  */
 int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,
                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -320,9 +320,9 @@ int32_t nia_qk_norm_rope_kv_write_fp8(void* q, int64_t q_tok_stride, int64_t q_h
  * rounding, the scale multiplies the q . k score, and each softmax weight carries its
  * row's v scale).  Same workspace contract as nia_paged_decode (its size with dtype
  * NIA_DTYPE_BF16); head_dim 128, any block_size >= 1, any num_heads / num_kv_heads
- * (as nia_paged_decode).  Block sizes that are powers of two >= 16 run the split
- * kernels; other sizes run the f32 path's kernel over rows dequantised on load as
- * code * row scale in fp32 (several times slower).
+ * (as nia_paged_decode).  Block sizes that are multiples of 16 run the split kernels
+ * (a 16-key tile in one block); other sizes run the f32 path's kernel over rows
+ * dequantised on load as code * row scale in fp32 (far slower).
  */
 int32_t nia_paged_decode_fp8(void* out, int64_t out_batch_stride, int64_t out_head_stride,
                              const void* q, int64_t q_batch_stride, int64_t q_head_stride,

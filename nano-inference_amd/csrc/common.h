@@ -43,6 +43,26 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // ---- bit casts --------------------------------------------------------------
 
+// Host: division of a key 0 <= x < 2^31 by the block size d >= 1 as mulhi(x, m) >> s: with
+// l = ceil(log2 d) and m = ceil(2^(31 + l) / d) (< 2^32 since d > 2^(l - 1)), m d - 2^(31 + l)
+// < d <= 2^l, so floor(x m / 2^(31 + l)) = floor(x / d) for every x < 2^31 (the round-up
+// method of Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994).  For d = 2^k it is m = 2^31, s = k - 1: the shift by k.
+inline void block_divisor(int32_t d, uint32_t& m, int32_t& s) {
+  if (d <= 1) {  // no 32-bit m divides by 1: every key maps to block 0 (the kernels that
+    m = 0;        // use this take block sizes >= 4; block size 1 is routed elsewhere)
+    s = 0;
+    return;
+  }
+  int l = 1;
+  while ((int64_t)1 << l < d) ++l;
+  m = (uint32_t)((((uint64_t)1 << (31 + l)) + (uint64_t)d - 1) / (uint64_t)d);
+  s = l - 1;
+}
+
+// Device: the block of key x under the divisor (m, s) of block_divisor.
+NIA_DEVICE int key_block(int x, uint32_t m, int s) { return (int)(__umulhi((uint32_t)x, m) >> s); }
+
 NIA_DEVICE float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 NIA_DEVICE uint32_t as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
 

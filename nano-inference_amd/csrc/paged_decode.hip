@@ -76,8 +76,11 @@ struct DecodeParams {
   float* ws_ml;  // [batch][num_heads][max_parts][2]  (m, l) in log2 units
   float* ws_o;   // [batch][num_heads][max_parts][D]   un-normalised partial output
   int32_t max_parts;
-  // split kernel
-  int32_t bs_log2;
+  // split kernel: the block size, and key / block size = mulhi(key, bs_magic) >> bs_shift
+  // for 0 <= key < 2^31 (block_divisor)
+  int32_t bs;
+  uint32_t bs_magic;
+  int32_t bs_shift;
   int32_t group;  // G = num_heads / num_kv_heads (split kernel: query heads of this launch per KV head)
   int32_t q_group;  // split kernel: heads between KV head groups in q and out (the call's G)
   int32_t hg;     // KV heads per workgroup
@@ -652,11 +655,11 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   __shared__ int s_wave[kDecodeWaves];
   // The parameters of the prologue and the first unit in one round of scalar loads (left to
   // itself the compiler loads each on first use, a round trip each before the first DMA).
-  asm volatile("" ::"s"(p.context_lens), "s"(p.max_blocks), "s"(p.bs_log2), "s"(p.ws_pfx),
+  asm volatile("" ::"s"(p.context_lens), "s"(p.max_blocks), "s"(p.bs), "s"(p.ws_pfx),
                "s"(p.grid), "s"(p.first_wgs), "s"(p.wph), "s"(p.hg), "s"(p.nhg),
                "s"(p.block_tables), "s"(p.bt_stride), "s"(p.group));
   asm volatile("" ::"s"(p.k_cache), "s"(p.v_cache), "s"(p.num_kv_heads), "s"(p.num_blocks),
-               "s"(p.q), "s"(p.q_b), "s"(p.q_h), "s"(p.q_group));
+               "s"(p.q), "s"(p.q_b), "s"(p.q_h), "s"(p.q_group), "s"(p.bs_magic), "s"(p.bs_shift));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   // wave-uniform, and said so: everything derived from it (the unit walk, block ids, buffer
@@ -664,9 +667,14 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
   const int wave = uniform(tid / kWave);
   const int hn = lane & 15;    // query head of the group in this lane's accumulator column
   const int quad = lane >> 4;  // rows (keys / dims) 4 quad .. + 3 of the accumulators
-  const int bs_log2 = p.bs_log2;
-  const int bs_mask = (1 << bs_log2) - 1;
-  const int64_t cap = (int64_t)p.max_blocks << bs_log2;
+  // a key's block and its row in the block (any block size the split kernels take)
+  const int bs = p.bs;
+  const uint32_t bs_magic = p.bs_magic;
+  const int bs_shift = p.bs_shift;
+  auto bdiv = [&](int key) __attribute__((always_inline)) -> int {
+    return (int)(__umulhi((uint32_t)key, bs_magic) >> bs_shift);
+  };
+  const int64_t cap = (int64_t)p.max_blocks * bs;
   const int G = p.group;
 
   // ---- units before each sequence (one head group), and the clamped context lengths -------
@@ -777,15 +785,16 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
       locate(x.u + 1, x);
     }
   };
-  // Lanes 0 .. 7: the table entries of a unit's 32 keys, blocks (32 j >> bs_log2) + lane;
+  // Lanes 0 .. 7: the table entries of a unit's 32 keys, blocks 32 j / bs + lane (a unit
+  // spans at most 8 blocks: 8 aligned ones at bs 4, at most 4 for larger block sizes);
   // -1 past the context or past the unit.  The entries are checked against [0, num_blocks)
   // where they are used: a check here would wait for the load (and with it for every load
   // in flight, the DMA of the next unit included).
   auto load_ids = [&](const SplitUnit& x) __attribute__((always_inline)) -> int {
     if (x.u < 0) return -1;
     const int k0 = kUnitKeys * x.j;
-    const int bi = (k0 >> bs_log2) + lane;
-    const int last = (min(k0 + kUnitKeys, x.ctx) - 1) >> bs_log2;
+    const int bi = bdiv(k0) + lane;
+    const int last = bdiv(min(k0 + kUnitKeys, x.ctx) - 1);
     int id = -1;
     if (lane < 8 && bi <= last) id = p.block_tables[(int64_t)x.b * p.bt_stride + bi];
     return id;
@@ -806,31 +815,32 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
     hk = uniform(hk);
     const int k0 = uniform(kUnitKeys * x.j);
     const int ctx = uniform(x.ctx);
-    const int bi0 = k0 >> bs_log2;
+    const int bi0 = bdiv(k0);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       uint8_t* part = slot + 8192 * t;
       if constexpr (FP8) {
-        // a tile lies in one block (block size >= 16)
+        // a tile lies in one block (block size a multiple of 16)
         const int key = k0 + 16 * t;
-        const int blk =
-            key < ctx ? valid_block(__builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0)) : -1;
+        const int kb = bdiv(key);
+        const int krow = key - kb * bs;
+        const int blk = key < ctx ? valid_block(__builtin_amdgcn_readlane(ids, kb - bi0)) : -1;
         // the scales are read for every tile (block 0's rows stand in for a missing block or
         // a tile past the context): the keys they belong to are masked where they are used,
         // and nothing here may consume the loads (that would wait for the DMA in flight)
-        const int64_t head = ((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << bs_log2;
-        const int64_t row0 = head + (key & bs_mask) + 4 * quad;
+        const int64_t head = ((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) * bs;
+        const int64_t row0 = head + krow + 4 * quad;
         ks[t] = *reinterpret_cast<const float4*>(p.k_scale + row0);
         vs[t] = *reinterpret_cast<const float4*>(p.v_scale + row0);
         if (blk >= 0) {
           const uint8_t* kb = reinterpret_cast<const uint8_t*>(p.k_cache) + head * 128;
           const uint8_t* vb = reinterpret_cast<const uint8_t*>(p.v_cache) + head * 128;
-          const int bytes = 128 << bs_log2;
+          const int bytes = 128 * bs;
           const __amdgpu_buffer_rsrc_t kr =
               __builtin_amdgcn_make_buffer_rsrc((void*)kb, 0, bytes, kBufferWord3);
           const __amdgpu_buffer_rsrc_t vr =
               __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, bytes, kBufferWord3);
-          const uint32_t soff = (uint32_t)(key & bs_mask) * 128u;
+          const uint32_t soff = (uint32_t)krow * 128u;
           // K: DMA d of lane l brings key l % 16, codes of dims 64 d + 16 quad .. + 15, to
           // 1024 d + 16 l (the A operand order); V: the codes as they are (rows 8 d + l / 8)
           const uint32_t ksrc = (uint32_t)(hn * 128 + 16 * quad);
@@ -843,19 +853,20 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int key = k0 + 16 * t + 4 * j;  // rows 4 j .. + 3 lie in one block (>= 4 rows)
-          const int blk =
-              key < ctx ? valid_block(__builtin_amdgcn_readlane(ids, (key >> bs_log2) - bi0)) : -1;
+          // rows 4 j .. + 3 lie in one block (block size a multiple of 4)
+          const int key = k0 + 16 * t + 4 * j;
+          const int kb = bdiv(key);
+          const int blk = key < ctx ? valid_block(__builtin_amdgcn_readlane(ids, kb - bi0)) : -1;
           if (blk >= 0) {
-            const int64_t head = ((int64_t)blk * p.num_kv_heads + hk) << bs_log2;
-            const int bytes = (D * 2) << bs_log2;
+            const int64_t head = ((int64_t)blk * p.num_kv_heads + hk) * bs;
+            const int bytes = (D * 2) * bs;
             const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
                 (void*)(reinterpret_cast<const bf16_t*>(p.k_cache) + head * D), 0, bytes,
                 kBufferWord3);
             const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
                 (void*)(reinterpret_cast<const bf16_t*>(p.v_cache) + head * D), 0, bytes,
                 kBufferWord3);
-            const uint32_t soff = (uint32_t)((key & bs_mask) * D * 2);
+            const uint32_t soff = (uint32_t)((key - kb * bs) * D * 2);
             if (off.dma_ok[j]) {
               lds_dma16_s(kr, off.src[j], soff, part + 1024 * j);
               lds_dma16_s(vr, off.src[j], soff, part + 4096 + 1024 * j);
@@ -994,13 +1005,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
 
     // ---- scores, masked past the context and in invalid blocks ------------------------------
     const int k0 = kUnitKeys * cur.j;
-    const int bi0 = k0 >> bs_log2;
+    const int bi0 = bdiv(k0);
     const uint32_t okmask =
         (uint32_t)__builtin_amdgcn_ballot_w64(valid_block(ids_c) >= 0) & 0xffu;
     bool blk_ok[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
-      blk_ok[t] = (okmask >> (((k0 + 16 * t + 4 * quad) >> bs_log2) - bi0)) & 1u;
+      blk_ok[t] = (okmask >> (bdiv(k0 + 16 * t + 4 * quad) - bi0)) & 1u;
     f32x4_t sc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -1106,7 +1117,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void decode_split_kernel(DecodeP
 // kernel's LDS (one workgroup, a running scan over chunks of the batch).
 __global__ __launch_bounds__(kDecodeThreads) void decode_prefix_kernel(DecodeParams p, int batch) {
   __shared__ int s_wave[kDecodeWaves];
-  const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+  const int64_t cap = (int64_t)p.max_blocks * p.bs;
   int base = 0;
   for (int c0 = 0; c0 < batch; c0 += kDecodeThreads) {
     const int b = c0 + (int)threadIdx.x;
@@ -1245,8 +1256,9 @@ size_t split_workspace(int32_t batch, int32_t num_kv_heads, int32_t group, int32
 }
 
 bool split_shape(bool fp8, int32_t head_dim, int32_t block_size, int32_t group) {
-  const bool pow2 = block_size > 0 && (block_size & (block_size - 1)) == 0;
-  if (!pow2 || block_size < (fp8 ? 16 : 4) || group < 1) return false;
+  // bf16: a DMA row group (4 keys) lies in one block; fp8: a 16-key tile does
+  const int32_t step = fp8 ? 16 : 4;
+  if (block_size < step || block_size % step != 0 || group < 1) return false;
   return fp8 ? head_dim == 128
              : (head_dim == 64 || head_dim == 80 || head_dim == 96 || head_dim == 128);
 }
@@ -1478,6 +1490,8 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
   // fit an int (the prefix sums), and all of them 2^36 (the fp64 range arithmetic); a batch
   // beyond that would stream more than 2^41 keys per head group.
   {
+    // keys are ints, and the block division is exact below 2^31
+    if ((int64_t)max_blocks_per_seq * block_size > INT32_MAX) return NIA_ERR_UNSUPPORTED;
     const int64_t per_seq = (((int64_t)max_blocks_per_seq * block_size) + kUnitKeys - 1) / kUnitKeys;
     const int64_t hgs = num_kv_heads % 4 == 0 ? 4 : (num_kv_heads % 2 == 0 ? 2 : 1);
     const int64_t units = per_seq * batch;
@@ -1490,7 +1504,8 @@ int32_t paged_decode_entry(void* out, int64_t out_batch_stride, int64_t out_head
     return NIA_ERR_MISALIGNED;
   // the fp8 loop reads a tile's row scales four at a time (16 bytes)
   if (fp8 && ((uintptr_t)k_scale % 16 || (uintptr_t)v_scale % 16)) return NIA_ERR_MISALIGNED;
-  p.bs_log2 = __builtin_ctz((unsigned)block_size);
+  p.bs = block_size;
+  block_divisor(block_size, p.bs_magic, p.bs_shift);
   p.hg = num_kv_heads % 4 == 0 ? 4 : (num_kv_heads % 2 == 0 ? 2 : 1);
   p.wph = 4 / p.hg;
   p.nhg = num_kv_heads / p.hg;

@@ -11,7 +11,7 @@
 // lacks (its prefill ignores the cache).
 //
 // Two kernels share the tiling below: prefill_dma_kernel (head_dim 64/80/96/128,
-// K/V tiles fetched by DMA into LDS; paged calls with block size >= 16 and
+// K/V tiles fetched by DMA into LDS; paged calls with block sizes that are multiples of 16 and
 // contiguous calls whose K/V token strides are below 2^26 elements) and
 // prefill_kernel (register-staged loads into a transposed V tile; the rest).
 //
@@ -69,7 +69,10 @@ struct PrefillParams {
   int32_t bt_stride;
   int32_t max_blocks;
   int64_t num_blocks;
-  int32_t bs_log2;
+  int32_t bs;        // block size; a key's block is key_block(key, bs_magic, bs_shift)
+  uint32_t bs_magic;
+  int32_t bs_shift;
+  int32_t bs_log2;   // power-of-two block sizes: log2 (the register-staged kernel's shift)
   int32_t num_heads;
   int32_t num_kv_heads;
   int32_t group;
@@ -166,7 +169,7 @@ NIA_DEVICE void rank_sequences(const PrefillParams& p, int* s_key, int* s_order)
     int key;
     if constexpr (PAGED) {
       const int64_t c = p.ctx_len[tid];
-      const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+      const int64_t cap = (int64_t)p.max_blocks * p.bs;
       key = (int)(c < 0 ? 0 : (c > cap ? cap : c));
     } else {
       key = p.k_len[tid];
@@ -201,7 +204,9 @@ NIA_DEVICE bool map_workgroup(const PrefillParams& p, int& seq, int& h, int& mb)
 // XOR swizzle of the 4-key groups inside a transposed-V row (row = head dim d).
 NIA_DEVICE int vt_swz(int d) { return (d ^ (d >> 3)) & 15; }
 
-template <int D, bool PAGED>
+// DIV: paged, with a block size that is not a power of two (a key's block by division; the
+// shift and mask of power-of-two sizes hold fewer registers live across the tile loads).
+template <int D, bool PAGED, bool DIV = false>
 __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillParams p) {
   constexpr int DK = D / 16;               // 16-wide head-dim steps of QK^T
   constexpr int DT = (D + 31) / 32;        // 32-row head-dim tiles of O^T
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
   int64_t kstart = 0;
   if constexpr (PAGED) {
     int64_t c = p.ctx_len[seq];
-    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    const int64_t cap = (int64_t)p.max_blocks * p.bs;
     c = c < 0 ? 0 : (c > cap ? cap : c);
     klen = (int)c;
   } else {
@@ -280,10 +285,18 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_kernel(PrefillPara
   auto row_ptr = [&](const bf16_t* base, int64_t tok_stride, int64_t head_stride,
                      int n) -> const bf16_t* {
     if constexpr (PAGED) {
-      const int blk = bt[n >> p.bs_log2];
-      if (blk < 0 || (int64_t)blk >= p.num_blocks) return nullptr;
-      const int off = n & ((1 << p.bs_log2) - 1);
-      return base + ((((int64_t)blk * p.num_kv_heads + hk) << p.bs_log2) + off) * D;
+      if constexpr (DIV) {
+        const int nb = key_block(n, p.bs_magic, p.bs_shift);
+        const int blk = bt[nb];
+        if (blk < 0 || (int64_t)blk >= p.num_blocks) return nullptr;
+        const int off = n - nb * p.bs;
+        return base + (((int64_t)blk * p.num_kv_heads + hk) * p.bs + off) * D;
+      } else {
+        const int blk = bt[n >> p.bs_log2];
+        if (blk < 0 || (int64_t)blk >= p.num_blocks) return nullptr;
+        const int off = n & ((1 << p.bs_log2) - 1);
+        return base + ((((int64_t)blk * p.num_kv_heads + hk) << p.bs_log2) + off) * D;
+      }
     } else {
       return base + (kstart + n) * tok_stride + (int64_t)hk * head_stride;
     }
@@ -506,13 +519,17 @@ constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
 // COMPACT (paired heads, D < 128): K/V rows keep their own D * 2 bytes in LDS (no swizzle)
 // instead of 256, so three workgroups fit a CU instead of two: the short windows are bound
 // by the latency of their loads, which more resident workgroups hide.
-template <int D, bool PAGED, bool PAIR = false, bool BIAS = false, bool COMPACT = false>
+// DIV: paged, with a block size that is a multiple of 16 but not a power of two (a key's
+// block by division instead of a shift).
+template <int D, bool PAGED, bool PAIR = false, bool BIAS = false, bool COMPACT = false,
+          bool DIV = false>
 __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_kernel(
     PrefillParams p) {
   static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
   static_assert(!(PAIR && PAGED), "paired heads read contiguous K/V");
   static_assert(!(BIAS && (PAIR || PAGED)), "masks apply to contiguous, unpaired calls");
   static_assert(!COMPACT || (PAIR && D < 128), "compact rows serve paired heads, D < 128");
+  static_assert(!DIV || PAGED, "block division serves paged calls");
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
@@ -572,7 +589,7 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
   int64_t kstart = 0;
   if constexpr (PAGED) {
     int64_t c = p.ctx_len[seq];
-    const int64_t cap = (int64_t)p.max_blocks << p.bs_log2;
+    const int64_t cap = (int64_t)p.max_blocks * p.bs;
     c = c < 0 ? 0 : (c > cap ? cap : c);
     klen = (int)c;
   } else {
@@ -618,7 +635,6 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
   const int ld_sub = lane >> 4;
   const int ld_pc = lane & 15;
   const int32_t* bt = PAGED ? p.block_tables + (int64_t)seq * p.bt_stride : nullptr;
-  const int bs_mask = (1 << p.bs_log2) - 1;
   // KV block holding this wave's 16-row group of tile n0 (first row clamped into the
   // context); -1 for an invalid id.
   // A scalar load: a vector load here would be waited for with vmcnt(0), which also waits
@@ -626,7 +642,9 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
   auto block_of = [&](int n0) __attribute__((always_inline)) -> int {
     if constexpr (PAGED) {
       using const_i32 = const __attribute__((address_space(4))) int32_t*;
-      const int b = ((const_i32)bt)[uniform(min(n0 + 16 * wave, klen - 1) >> p.bs_log2)];
+      const int key = min(n0 + 16 * wave, klen - 1);
+      const int b = ((const_i32)bt)[uniform(DIV ? key_block(key, p.bs_magic, p.bs_shift)
+                                                : key >> p.bs_log2)];
       return (b < 0 || (int64_t)b >= p.num_blocks) ? -1 : b;
     } else {
       return 0;
@@ -656,7 +674,9 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
                       int blk) __attribute__((always_inline)) -> const bf16_t* {
     if constexpr (PAGED) {
       const int64_t r =
-          ((((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) << p.bs_log2) + (row & bs_mask));
+          (((int64_t)(blk < 0 ? 0 : blk) * p.num_kv_heads + hk) * p.bs +
+           (DIV ? row - key_block(row, p.bs_magic, p.bs_shift) * p.bs
+                : row & ((1 << p.bs_log2) - 1)));
       return base + r * D;
     } else {
       return base + (kstart + row) * tok + (int64_t)hk * head;
@@ -1018,6 +1038,16 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
 
 constexpr int64_t kMaxRowStride = (int64_t)1 << 26;  // elements
 
+// The register-staged kernel: paged calls whose block size is not a power of two take the
+// division variant.
+template <int D, bool PAGED>
+void launch_staged(const PrefillParams& p, dim3 grid, hipStream_t s) {
+  if (PAGED && (p.bs & (p.bs - 1)))
+    nia_launch((prefill_kernel<D, PAGED, PAGED>), grid, dim3(kPrefillThreads), s, p);
+  else
+    nia_launch((prefill_kernel<D, PAGED>), grid, dim3(kPrefillThreads), s, p);
+}
+
 template <bool PAGED, bool BIAS = false>
 int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream_t s) {
   const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd * p.group * p.num_m_blocks;
@@ -1026,7 +1056,7 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
   // The DMA kernel needs 16-row groups inside one KV block and 32-bit lane offsets;
   // the register-staged kernel serves the rest.
   const bool dma_ok = p.q_tok >= 0 && p.q_tok < kMaxRowStride &&
-                      (PAGED ? p.bs_log2 >= 4
+                      (PAGED ? p.bs % 16 == 0
                              : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
                                 p.v_tok < kMaxRowStride));
   if (BIAS && !dma_ok) return NIA_ERR_UNSUPPORTED;
@@ -1036,10 +1066,13 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
     if (BIAS)                                                                                \
       nia_launch((prefill_dma_kernel<DD, false, false, true>), grid, dim3(kPrefillThreads),  \
                  s, p);                                                                      \
+    else if (dma_ok && PAGED && (p.bs & (p.bs - 1)))                                         \
+      nia_launch((prefill_dma_kernel<DD, PAGED, false, false, false, PAGED>), grid,          \
+                 dim3(kPrefillThreads), s, p);                                               \
     else if (dma_ok)                                                                         \
       nia_launch((prefill_dma_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), s, p);        \
     else                                                                                     \
-      nia_launch((prefill_kernel<DD, PAGED>), grid, dim3(kPrefillThreads), s, p);            \
+      launch_staged<DD, PAGED>(p, grid, s);                                                  \
     break;
     NIA_PREFILL_CASE(64)
     NIA_PREFILL_CASE(80)
@@ -1255,10 +1288,10 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
   // the key positions of a sequence (table width x block size) must fit an int
   if ((int64_t)max_blocks_per_seq * block_size > INT32_MAX) return NIA_ERR_UNSUPPORTED;
   if (dtype != NIA_DTYPE_F32 && dtype != NIA_DTYPE_BF16) return NIA_ERR_UNSUPPORTED;
-  if (dtype == NIA_DTYPE_F32 || (block_size & (block_size - 1))) {
-    // fp32, and bf16 block sizes that are not powers of two (the bf16 kernel finds a row's
-    // block and slot with a shift and a mask): the fp32 kernel, which maps every key through
-    // the table on its own (any block size), reading bf16 rows where the cache holds them
+  if (dtype == NIA_DTYPE_F32 || block_size == 1) {
+    // fp32, and bf16 at block size 1 (the bf16 kernels divide keys by the block size with a
+    // 32-bit multiplier, which block size 1 does not have): the fp32 kernel, which maps every
+    // key through the table on its own, reading bf16 rows where the cache holds them
     const bool f32 = dtype == NIA_DTYPE_F32;
     if (f32 ? (!vec_ok_f32(q, q_tok_stride, q_head_stride) ||
                !vec_ok_f32(out, out_tok_stride, out_head_stride) || (uintptr_t)k_cache % 16 ||
@@ -1292,7 +1325,8 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
     return launch_prefill_f32(f, true, head_dim, num_seqs, max_q_len, (hipStream_t)stream,
                               f32 ? kElemF32 : kElemBf16);
   }
-  // bf16, power-of-two block sizes: a row's block and slot are a shift and a mask
+  // bf16, block size >= 2: a key's block is a multiply-shift division (block_divisor); block
+  // sizes that are multiples of 16 keep a wave's 16-row DMA group in one block
   if (!vec_ok(q, q_tok_stride, q_head_stride) || !vec_ok(out, out_tok_stride, out_head_stride) ||
       (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
     return NIA_ERR_MISALIGNED;
@@ -1312,7 +1346,9 @@ extern "C" int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t 
   p.bt_stride = bt_stride;
   p.max_blocks = max_blocks_per_seq;
   p.num_blocks = num_blocks;
-  p.bs_log2 = __builtin_ctz((unsigned)block_size);
+  p.bs = block_size;
+  block_divisor(block_size, p.bs_magic, p.bs_shift);
+  p.bs_log2 = (block_size & (block_size - 1)) ? 0 : __builtin_ctz((unsigned)block_size);
   p.num_heads = num_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = num_heads / num_kv_heads;

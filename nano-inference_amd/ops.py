@@ -210,10 +210,11 @@ def check_pool_shape(head_dim: int, block_size: int, num_heads: int, num_kv_head
     * fp8 caches: head_dim 128, any block size and group.
 
     Any positive block size is taken, as the reference's (a free integer,
-    src/nano_inference/core/config.py:54; 16 is its default).  The tuned bf16 / fp8 kernels
-    find a key's block and slot with a shift and a mask: bf16 block sizes that are powers of
-    two >= 4 (fp8: >= 16) run them, other sizes run the fp32-softmax kernel that maps every
-    key through the table on its own (correct, several times slower)."""
+    src/nano_inference/core/config.py:54; 16 is its default).  The tuned kernels find a
+    key's block by a multiply-shift division: bf16 decode takes block sizes that are
+    multiples of 4 (fp8: of 16), bf16 chunked prefill any size >= 2 (multiples of 16 by DMA);
+    other sizes run the fp32-softmax kernel that maps every key through the table on its
+    own (correct, far slower)."""
     if num_kv_heads <= 0 or num_heads <= 0 or num_heads % num_kv_heads != 0:
         raise ValueError(f"num_heads must be divisible by num_kv_heads, got {num_heads=} and "
                          f"{num_kv_heads=}")

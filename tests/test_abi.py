@@ -57,8 +57,8 @@ def test_validation_returns_codes_without_launching():
                                 None, 0, 0, None) == _lib.ERR_UNSUPPORTED
     assert lib.nia_paged_decode(p, 0, 0, p, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 72, 12, 10, 0.1,
                                 None, 0, 0, None) == _lib.ERR_UNSUPPORTED
-    # bf16 block sizes 2 and 12 take the any-size kernel, whose checks see a q that is not
-    # 8-byte aligned
+    # bf16 block size 2 takes the any-size kernel and 12 the split kernels: both refuse a q
+    # that is not 8-byte aligned
     odd = ctypes.c_void_p(18)
     for bs in (2, 12):
         assert lib.nia_paged_decode(p, 0, 0, odd, 0, 0, p, p, p, 4, 4, p, 2, 8, 4, 128, bs, 10,
@@ -84,8 +84,8 @@ def test_validation_returns_codes_without_launching():
                            5, 0, None) == _lib.ERR_INVALID_ARGUMENT
     assert lib.nia_prefill(p, 8, 8, p, 8, 8, p, 8, 8, p, 8, 8, p, p, p, p, 1, 4, 2, 2, 128, 0.0,
                            1, 0, None) == _lib.ERR_INVALID_ARGUMENT
-    # paged prefill: a bf16 block size that is not a power of two takes the any-size
-    # kernel (its checks see the unaligned q); an unsupported head_dim is refused first
+    # paged prefill: a bf16 block size that is not a power of two takes the MFMA kernels
+    # (their checks see the unaligned q); an unsupported head_dim is refused first
     assert lib.nia_prefill_paged(p, 8, 8, ctypes.c_void_p(18), 8, 8, p, p, p, 4, 4, p, p, p, 1,
                                  4, 2, 2, 128, 12, 10, 0.1, 2, 0, None) == _lib.ERR_MISALIGNED
     assert lib.nia_prefill_paged(p, 8, 8, p, 8, 8, p, p, p, 4, 4, p, p, p, 1, 4, 2, 2, 72, 12,
@@ -128,10 +128,13 @@ def test_workspace_size():
         hdr + 64 * 32 * 16 * 130 * 4
     # fp32 other shapes run without partials
     assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, 32, 128, 1) == hdr
-    # bf16 block sizes the split kernels do not take run the any-size kernel, without
-    # partials either
-    for bs in (1, 2, 12, 24, 48):
+    # bf16 block sizes the split kernels do not take (not multiples of 4) run the any-size
+    # kernel, without partials either; multiples of 4 take the split kernels' workspace
+    for bs in (1, 2, 3, 5, 6, 10, 22):
         assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, bs, 128, 0) == hdr
+    for bs in (12, 24, 48, 100):
+        assert lib.nia_paged_decode_workspace_size(64, 32, 8, 512, bs, 128, 0) == \
+            hdr + pfx + rec + 512 * 8 * 4 * 130 * 4
     assert lib.nia_paged_decode_workspace_size(64, 32, 3, 512, 16, 128, 0) == 0  # 32 % 3
 
 

@@ -71,8 +71,9 @@ def test_bf16_block_sizes(bs):
                                                    (2, 96, 2, 20), (1, 128, 8, 1),
                                                    (100, 128, 1, 16)])
 def test_bf16_block_sizes_not_powers_of_two(bs, head_dim, hkv, group):
-    """Block sizes the split kernels do not take (not powers of two, or below 4; the
-    reference's is any positive integer): the any-size kernel over the bf16 rows, at
+    """Block sizes that are not powers of two (the reference's is any positive integer):
+    multiples of 4 (12, 24, 48, 100) on the split kernels, whose key-to-block step is a
+    multiply-shift division, the rest (5, 2, 1) on the any-size kernel over the bf16 rows, at
     several head dims and groups (20 beyond the split kernels' 16 MFMA columns)."""
     lens = edge_lens(bs)
     c = workloads.make_decode(len(lens), hkv * group, hkv, head_dim, lens,
@@ -192,10 +193,10 @@ def test_bf16_invalid_block_ids_are_skipped():
         assert_attn_close(out, exp, torch.bfloat16, f"invalid ids bs={bs}")
 
 
-@pytest.mark.parametrize("bs", [32, 64, 8, 12, 24, 1])
+@pytest.mark.parametrize("bs", [32, 64, 48, 8, 12, 24, 1])
 def test_fp8_block_sizes(bs):
-    """fp8 caches at block sizes 32 and 64 (split kernels) and 8, 12, 24, 1 (the any-size
-    kernel, rows dequantised on load)."""
+    """fp8 caches at block sizes 32, 64 and 48 (split kernels: multiples of 16, a tile in
+    one block) and 8, 12, 24, 1 (the any-size kernel, rows dequantised on load)."""
     from tests.test_gpu_fp8_kv import oracle_decode_fp8
     lens = edge_lens(bs)
     c = workloads.make_decode(len(lens), 16, 4, 128, lens, sum(-(-L // bs) for L in lens) + 9, bs,

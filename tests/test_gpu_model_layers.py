@@ -163,13 +163,15 @@ class PackedStepper:
         return out, exp
 
 
-@pytest.mark.parametrize("bs", [16, 128, 256, 24])
+@pytest.mark.parametrize("bs", [16, 128, 256, 24, 48])
 @pytest.mark.parametrize("fp8", [False, True])
 def test_packed_step_qwen3_0p6b_layer(fp8, bs):
     """Three packed steps (prefill chunks, then decodes mixed with chunks, then decodes),
     block sizes 16, 128 and 256: with the larger blocks most chunks and decode rows sit
-    inside one block and some cross into the next.  Block size 24 (not a power of two)
-    takes the any-size kernel for the decode rows and the bf16 chunks."""
+    inside one block and some cross into the next.  Block sizes 24 and 48 (not powers of
+    two) run the split decode and, for the chunks, the register-staged (24) and DMA (48)
+    prefill kernels over bf16 pools; over fp8 pools the decode at 24 takes the any-size
+    kernel."""
     torch.manual_seed(10)
     m = PagedCausalSelfAttention(1024, 16, num_kv_heads=8, head_dim=128, use_qk_norm=True,
                                  rope_base=1e6).to("cuda", torch.bfloat16).eval()

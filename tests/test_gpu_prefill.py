@@ -223,11 +223,14 @@ def test_chunked_prefill_block_sizes_full(bs):
         assert_attn_close(o[s * c.chunk + idx], ref, torch.bfloat16, f"bs {bs} chunk {s}")
 
 
-@pytest.mark.parametrize("bs,group", [(1, 4), (5, 4), (12, 4), (24, 7), (100, 2)])
+@pytest.mark.parametrize("bs,group", [(1, 4), (5, 4), (12, 4), (24, 7), (100, 2), (48, 4),
+                                      (80, 2)])
 def test_chunked_prefill_other_block_sizes_full(bs, group):
     """Block sizes that are not powers of two (the reference's block size is any positive
-    integer, src/nano_inference/core/config.py:54), which the any-size kernel takes over
-    the bf16 rows: prior lengths on both sides of block edges, every row checked."""
+    integer, src/nano_inference/core/config.py:54): multiples of 16 (48, 80) on the DMA
+    kernel, others of at least 2 on the register-staged kernel (both divide keys by the block
+    size), block size 1 on the fp32-softmax kernel: prior lengths on both sides of block
+    edges, every row checked."""
     prior = [0, 1, max(bs - 1, 0), bs, bs + 1, 3 * bs + 7]
     c = workloads.chunked_qwen3_8b("cuda", n=6, chunk=80, prior=prior, num_heads=2 * group,
                                    num_kv_heads=2, block_size=bs)
