@@ -214,10 +214,10 @@ int32_t nia_prefill_masked(void* out, int64_t out_tok_stride, int64_t out_head_s
  * NIA_CAUSAL_BOTTOM_RIGHT; NIA_CAUSAL_NONE lets every row see the whole context.
  * Supported: head_dim 64, 80, 96 or 128; dtype bf16 or f32 with any block_size >= 1
  * and max_blocks_per_seq * block_size < 2^31 (keys in blocks outside [0, num_blocks)
- * are skipped).  bf16 block sizes >= 2 run the MFMA kernels (multiples of 16 stream
- * 16-row groups of a block into LDS by DMA, other sizes take register-staged loads,
- * ~2.5x slower); bf16 block size 1, and f32, run the f32 kernel (q . k in fp64, bf16
- * rows widened on load).
+ * are skipped).  bf16 block sizes >= 2 run the MFMA kernels (multiples of 4 stream rows
+ * into LDS by DMA, 16-row groups of a block or, when 16 does not divide the block size,
+ * 4-row groups; other sizes take register-staged loads, ~2.5x slower); bf16 block size
+ * 1, and f32, run the f32 kernel (q . k in fp64, bf16 rows widened on load).
  */
 int32_t nia_prefill_paged(void* out, int64_t out_tok_stride, int64_t out_head_stride,
                           const void* q, int64_t q_tok_stride, int64_t q_head_stride,

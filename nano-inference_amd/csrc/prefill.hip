@@ -520,9 +520,11 @@ constexpr int kTileBytes = kBlockN * kTileRowBytes;  // 16 KB
 // instead of 256, so three workgroups fit a CU instead of two: the short windows are bound
 // by the latency of their loads, which more resident workgroups hide.
 // DIV: paged, with a block size that is a multiple of 16 but not a power of two (a key's
-// block by division instead of a shift).
+// block by division instead of a shift).  QUAD (with DIV): a multiple of 4 but not of 16, so
+// a wave's 16-row DMA group may cross blocks: each DMA instruction (4 rows, which lie in
+// one block) gets the block and buffer resource of its own rows.
 template <int D, bool PAGED, bool PAIR = false, bool BIAS = false, bool COMPACT = false,
-          bool DIV = false>
+          bool DIV = false, bool QUAD = false>
 __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_kernel(
     PrefillParams p) {
   static_assert(D % 16 == 0 && D <= 128, "head_dim a multiple of 16, at most 128");
@@ -530,6 +532,7 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
   static_assert(!(BIAS && (PAIR || PAGED)), "masks apply to contiguous, unpaired calls");
   static_assert(!COMPACT || (PAIR && D < 128), "compact rows serve paired heads, D < 128");
   static_assert(!DIV || PAGED, "block division serves paged calls");
+  static_assert(!QUAD || DIV, "4-row groups take a key's block by division");
   constexpr int DK = D / 16;              // QK steps of 16 dims
   constexpr int DT = (D + 31) / 32;       // PV output tiles of 32 dims (the last one padded)
   constexpr int kChunks = D / 8;          // 16-byte chunks per K/V row
@@ -639,8 +642,23 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
   // context); -1 for an invalid id.
   // A scalar load: a vector load here would be waited for with vmcnt(0), which also waits
   // for the tile DMA just issued.
-  auto block_of = [&](int n0) __attribute__((always_inline)) -> int {
-    if constexpr (PAGED) {
+  struct BlkIds {
+    int b[4];
+  };
+  using BlkT = std::conditional_t<QUAD, BlkIds, int>;
+  auto block_of = [&](int n0) __attribute__((always_inline)) -> BlkT {
+    if constexpr (QUAD) {
+      // the blocks of the wave's four 4-row groups (first rows clamped into the context)
+      using const_i32 = const __attribute__((address_space(4))) int32_t*;
+      BlkIds r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = min(n0 + 16 * wave + 4 * i, klen - 1);
+        const int b = ((const_i32)bt)[uniform(key_block(key, p.bs_magic, p.bs_shift))];
+        r.b[i] = (b < 0 || (int64_t)b >= p.num_blocks) ? -1 : b;
+      }
+      return r;
+    } else if constexpr (PAGED) {
       using const_i32 = const __attribute__((address_space(4))) int32_t*;
       const int key = min(n0 + 16 * wave, klen - 1);
       const int b = ((const_i32)bt)[uniform(DIV ? key_block(key, p.bs_magic, p.bs_shift)
@@ -686,26 +704,48 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
   // resource spans exactly the 16 rows (a read past it would return zeros, never
   // fault).  Rows past the context repeat the last key (masked later).
   auto issue_rows = [&](const bf16_t* base, int64_t tok, int64_t head, int64_t row_stride,
-                        const uint32_t* lane_off, uint8_t* tile, int n0, int blk,
+                        const uint32_t* lane_off, uint8_t* tile, int n0, BlkT blk,
                         int grp) __attribute__((always_inline)) {
     uint8_t* dst = tile + grp * 16 * kTileRowBytes;
     const int g0 = n0 + 16 * grp;
-    const int gk = min(g0, klen - 1);
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)row_base(base, tok, head, gk, blk), 0, (int)((15 * row_stride + D) * 2),
-        kBufferWord3);
-    if (g0 + 15 < klen) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (kChunks == 16 || chunk_ok[i]) lds_dma16(rsrc, lane_off[i], dst + i * 1024);
-    } else {
+    if constexpr (QUAD) {
+      // instruction i's 4 rows from their own block, through a resource spanning them (the
+      // lane offsets drop the 4 i rows that lane_off counts from the group's first row)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 4 * i + ld_sub;
-        const int dr = min(g0 + r, klen - 1) - gk;
-        if (kChunks == 16 || chunk_ok[i])
-          lds_dma16(rsrc, (uint32_t)(dr * row_stride + 8 * (ld_pc ^ tile_swz(r))) * 2u,
-                    dst + i * 1024);
+        const int gi = g0 + 4 * i;
+        const int gki = min(gi, klen - 1);
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)row_base(base, tok, head, gki, blk.b[i]), 0, (int)((3 * row_stride + D) * 2),
+            kBufferWord3);
+        uint32_t off;
+        if (gi + 3 < klen) {
+          off = lane_off[i] - (uint32_t)(4 * i * row_stride * 2);
+        } else {
+          const int r = 4 * i + ld_sub;
+          const int dr = min(g0 + r, klen - 1) - gki;
+          off = (uint32_t)(dr * row_stride + 8 * (ld_pc ^ tile_swz(r))) * 2u;
+        }
+        if (kChunks == 16 || chunk_ok[i]) lds_dma16(rsrc, off, dst + i * 1024);
+      }
+    } else {
+      const int gk = min(g0, klen - 1);
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)row_base(base, tok, head, gk, blk), 0, (int)((15 * row_stride + D) * 2),
+          kBufferWord3);
+      if (g0 + 15 < klen) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kChunks == 16 || chunk_ok[i]) lds_dma16(rsrc, lane_off[i], dst + i * 1024);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * i + ld_sub;
+          const int dr = min(g0 + r, klen - 1) - gk;
+          if (kChunks == 16 || chunk_ok[i])
+            lds_dma16(rsrc, (uint32_t)(dr * row_stride + 8 * (ld_pc ^ tile_swz(r))) * 2u,
+                      dst + i * 1024);
+        }
       }
     }
   };
@@ -727,7 +767,7 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
       lds_dma16(rsrc, (uint32_t)(dr * tok + 8 * ch) * 2u, tile + 32 * wrow * kPitch + 1024 * t);
     }
   };
-  auto issue_tile = [&](int n0, int stage, int blk) __attribute__((always_inline)) {
+  auto issue_tile = [&](int n0, int stage, BlkT blk) __attribute__((always_inline)) {
     issue_rows(p.k, p.k_tok, p.k_head, k_row, k_lane, tile_k(stage), n0, blk, wave);
     issue_rows(p.v, p.v_tok, p.v_head, v_row, v_lane, tile_v(stage), n0, blk, wave);
   };
@@ -990,7 +1030,7 @@ __global__ __launch_bounds__(kPrefillThreads, COMPACT ? 3 : 2) void prefill_dma_
         }
       }
     }
-    int blk_nxt = block_of(0);
+    BlkT blk_nxt = block_of(0);
     issue_tile(0, 0, blk_nxt);
     if (kBlockN < n_end) blk_nxt = block_of(kBlockN);
     __builtin_amdgcn_s_waitcnt(0);
@@ -1053,10 +1093,11 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
   const int64_t nwg = (int64_t)kXcds * p.groups_per_xcd * p.group * p.num_m_blocks;
   if (nwg >= ((int64_t)1 << 31)) return NIA_ERR_UNSUPPORTED;
   const dim3 grid((unsigned)nwg);
-  // The DMA kernel needs 16-row groups inside one KV block and 32-bit lane offsets;
-  // the register-staged kernel serves the rest.
+  // The DMA kernel needs 4-row groups inside one KV block (block sizes that are multiples of
+  // 4; 16-row groups for the shift and DIV forms, 4-row ones for QUAD) and 32-bit lane
+  // offsets; the register-staged kernel serves the rest.
   const bool dma_ok = p.q_tok >= 0 && p.q_tok < kMaxRowStride &&
-                      (PAGED ? p.bs % 16 == 0
+                      (PAGED ? p.bs % 4 == 0
                              : (p.k_tok >= 0 && p.k_tok < kMaxRowStride && p.v_tok >= 0 &&
                                 p.v_tok < kMaxRowStride));
   if (BIAS && !dma_ok) return NIA_ERR_UNSUPPORTED;
@@ -1066,6 +1107,9 @@ int launch_prefill(const PrefillParams& p, int head_dim, int num_seqs, hipStream
     if (BIAS)                                                                                \
       nia_launch((prefill_dma_kernel<DD, false, false, true>), grid, dim3(kPrefillThreads),  \
                  s, p);                                                                      \
+    else if (dma_ok && PAGED && p.bs % 16 != 0)                                              \
+      nia_launch((prefill_dma_kernel<DD, PAGED, false, false, false, PAGED, PAGED>), grid,   \
+                 dim3(kPrefillThreads), s, p);                                               \
     else if (dma_ok && PAGED && (p.bs & (p.bs - 1)))                                         \
       nia_launch((prefill_dma_kernel<DD, PAGED, false, false, false, PAGED>), grid,          \
                  dim3(kPrefillThreads), s, p);                                               \

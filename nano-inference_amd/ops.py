@@ -212,7 +212,7 @@ def check_pool_shape(head_dim: int, block_size: int, num_heads: int, num_kv_head
     Any positive block size is taken, as the reference's (a free integer,
     src/nano_inference/core/config.py:54; 16 is its default).  The tuned kernels find a
     key's block by a multiply-shift division: bf16 decode takes block sizes that are
-    multiples of 4 (fp8: of 16), bf16 chunked prefill any size >= 2 (multiples of 16 by DMA);
+    multiples of 4 (fp8: of 16), bf16 chunked prefill any size >= 2 (multiples of 4 by DMA);
     other sizes run the fp32-softmax kernel that maps every key through the table on its
     own (correct, far slower)."""
     if num_kv_heads <= 0 or num_heads <= 0 or num_heads % num_kv_heads != 0:
